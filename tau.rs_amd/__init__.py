@@ -1,0 +1,8 @@
+"""tau.rs_amd: MI355X-native MoE expert-FFN path (HIP for gfx950 behind a C ABI).
+
+Load as a package named ``tau_rs_amd`` (the directory name holds a dot); see
+``tests/conftest.py`` and ``__graft_entry__.py``.
+"""
+from . import ffi, inputs, sparse_moe  # noqa: F401
+from .sparse_moe import (MoePrefillRunner, MoePrefillTile, SharedExpertConfig, SparseMoeBlock,  # noqa: F401
+                         SparseMoeConfig, moe_prefill_capacity)

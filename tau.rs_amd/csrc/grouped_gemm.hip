@@ -1,0 +1,455 @@
+// Grouped expert GEMMs for the MoE path on CDNA4 (gfx950).
+//
+// Both projections compute out[row, n] = sum_k A[row, k] * W[e][n, k] with A
+// and W K-contiguous ("NT"), BF16 operands and FP32 accumulators, over the
+// expert-major row blocks produced by dispatch (tiles[m] = expert of the
+// m-th M-row block).  The reference's grouped kernel and epilogues are
+// crates/cuda-kernels/src/kernels/moe_gemm.cu:63-138 and
+// linear_bf16_fp32.cu:47-98; the numerical contract kept here is:
+//   gate_up : gu = bf16(acc), a = bf16(silu(g) * u)   (fused, no [cap,2I] pass)
+//   down    : c[slot] = bf16(acc * w[slot])           (weight before the round)
+//
+// Two kernel families:
+//  * lds_gemm   -- prefill.  BM x BN x 64 block tile, 4 waves, each wave a grid
+//                  of 32x32x16 MFMAs; A/B panels staged through a double-
+//                  buffered LDS (row stride 72 BF16 to spread banks) with the
+//                  next K panel prefetched into registers during the MFMAs.
+//                  Gate_up B panels hold BN/2 gate rows then the matching
+//                  BN/2 up rows, so each lane owns (g, u) pairs for SiLU.
+//  * stream_gemm -- decode / small groups.  One wave per (16-row block,
+//                  16 output columns): expert weights are streamed from HBM
+//                  straight into 16x16x32 MFMA A-operands with 128-bit loads
+//                  (no LDS), several K steps in flight per wave.
+// Work items are mapped XCD-major (consecutive items on one XCD's L2) and the
+// number of live M blocks is read on the device from the dispatch metadata,
+// so no host readback is needed and dead capacity costs one early exit.
+#include "kernels.hpp"
+
+namespace tau_amd {
+
+namespace {
+
+template <bool Aligned>
+__device__ __forceinline__ u32x4 load_chunk(const uint16_t* row, int k, int K, bool valid) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (!valid) return v;
+    if constexpr (Aligned) {
+        if (k < K) v = *(const u32x4*)(row + k);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            uint32_t lo = k + j < K ? row[k + j] : 0u;
+            uint32_t hi = k + j + 1 < K ? row[k + j + 1] : 0u;
+            v[j / 2] = lo | (hi << 16);
+        }
+    }
+    return v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ int live_blocks(const GemmArgs& p, int bm) {
+    const int cap_blocks = (p.rows + bm - 1) / bm;
+    if (!p.meta_total) return cap_blocks;
+    const int used = (p.meta_total[0] + bm - 1) / bm;
+    return used < cap_blocks ? used : cap_blocks;
+}
+
+// ---------------------------------------------------------------------------
+// LDS-tiled MFMA kernel (prefill)
+// ---------------------------------------------------------------------------
+constexpr int kBK = 64;
+constexpr int kLdsStride = kBK + 8;  // BF16 elements per staged row
+
+template <int BM, int BN, int WM, int WN, int AM, int EPI, bool Aligned>
+__global__ __launch_bounds__(64 * WM * WN) void lds_gemm(GemmArgs p) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
+    constexpr int MI = TM / 32, NI = TN / 32;   // 32x32 MFMA blocks per wave
+    static_assert(MI >= 1 && NI >= 1, "wave tile too small");
+    static_assert(EPI != kEpiSilu || NI % 2 == 0, "SiLU pairs gate/up blocks");
+    constexpr int ACH = BM * (kBK / 8) / NT;     // 16-byte chunks per thread
+    constexpr int BCH = BN * (kBK / 8) / NT;
+    static_assert(ACH * NT == BM * kBK / 8 && BCH * NT == BN * kBK / 8, "tile/threads mismatch");
+    constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;  // output columns per block
+
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsStride];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kLdsStride];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    if (p.receipt && blockIdx.x == 0 && tid == 0) {
+        p.receipt[0] = BM; p.receipt[1] = BN; p.receipt[2] = kBK; p.receipt[3] = WM * WN; p.receipt[4] = 2;
+    }
+    const int n_tiles = (p.n + NOUT - 1) / NOUT;
+    const int live = live_blocks(p, BM);
+    const int total = live * n_tiles;
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    const int item = xcd_remap(blockIdx.x, per_xcd);
+    if (item >= total) return;
+    const int m_tile = item / n_tiles, n_tile = item - m_tile * n_tiles;
+    const int expert = p.tiles ? p.tiles[m_tile] : 0;
+    const int row0 = m_tile * BM;
+    const int c0 = n_tile * NOUT;
+
+    if (expert < 0) {
+        if constexpr (EPI == kEpiStoreBf16) {  // dead capacity reads as zeros
+            uint16_t* out = (uint16_t*)p.out;
+            for (int i = tid; i < BM * NOUT; i += NT) {
+                const int r = row0 + i / NOUT, c = c0 + i % NOUT;
+                if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
+            }
+        }
+        return;
+    }
+
+    // Per-thread A/B chunk sources, fixed across K.
+    const uint16_t* a_src[ACH];
+    bool a_ok[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+        const int c = tid + i * NT, r = c / (kBK / 8);
+        const int row = row0 + r;
+        bool ok = row < p.rows;
+        long src_row = row;
+        if constexpr (AM == kAGather) {
+            const int slot = ok ? p.slots[row] : p.assignments;
+            ok = slot >= 0 && slot < p.assignments;
+            src_row = ok ? slot / p.topk : 0;
+        }
+        a_ok[i] = ok;
+        a_src[i] = p.a + src_row * (long)p.lda;
+    }
+    const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
+    const uint16_t* b_src[BCH];
+    bool b_ok[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+        const int c = tid + i * NT, r = c / (kBK / 8);
+        long wrow;
+        bool ok;
+        if constexpr (EPI == kEpiSilu) {
+            const int j = c0 + (r < BN / 2 ? r : r - BN / 2);
+            ok = j < p.n;
+            wrow = (r < BN / 2 ? j : j + p.w_up_offset);
+        } else {
+            const int j = c0 + r;
+            ok = j < p.n;
+            wrow = j;
+        }
+        b_ok[i] = ok;
+        b_src[i] = wexp + (ok ? wrow : 0) * (long)p.k;
+    }
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+
+    u32x4 ra[ACH], rb[BCH];
+    const int nk = (p.k + kBK - 1) / kBK;
+    auto gload = [&](int kt) {
+        const int kb = kt * kBK;
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) {
+            const int kc = ((tid + i * NT) % (kBK / 8)) * 8;
+            ra[i] = load_chunk<Aligned>(a_src[i], kb + kc, p.k, a_ok[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int kc = ((tid + i * NT) % (kBK / 8)) * 8;
+            rb[i] = load_chunk<Aligned>(b_src[i], kb + kc, p.k, b_ok[i]);
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) {
+            const int c = tid + i * NT;
+            *(u32x4*)&As[buf][(c / (kBK / 8)) * kLdsStride + (c % (kBK / 8)) * 8] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int c = tid + i * NT;
+            *(u32x4*)&Bs[buf][(c / (kBK / 8)) * kLdsStride + (c % (kBK / 8)) * 8] = rb[i];
+        }
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int lrow = lane & 31, lk = (lane >> 5) * 8;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            bf16x8 af[MI], bfr[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                af[i] = as_bf16x8(*(const u32x4*)&As[buf][(wm * TM + i * 32 + lrow) * kLdsStride + ks * 16 + lk]);
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                int brow;
+                if constexpr (EPI == kEpiSilu) {
+                    // first NI/2 blocks: gate rows, last NI/2: matching up rows
+                    const int jj = j < NI / 2 ? j : j - NI / 2;
+                    brow = (j < NI / 2 ? 0 : BN / 2) + wn * (TN / 2) + jj * 32 + lrow;
+                } else {
+                    brow = wn * TN + j * 32 + lrow;
+                }
+                bfr[j] = as_bf16x8(*(const u32x4*)&Bs[buf][brow * kLdsStride + ks * 16 + lk]);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue.  32x32 accumulator layout: value q of lane l sits at
+    // row (q/4)*8 + (l/32)*4 + q%4, column l%32 of its block.
+    const int lcol = lane & 31, lr4 = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int r = row0 + wm * TM + i * 32 + (q >> 2) * 8 + lr4 + (q & 3);
+            if (r >= p.rows) continue;
+            if constexpr (EPI == kEpiSilu) {
+                uint16_t* out = (uint16_t*)p.out;
+#pragma unroll
+                for (int j = 0; j < NI / 2; ++j) {
+                    const int c = c0 + wn * (TN / 2) + j * 32 + lcol;
+                    if (c < p.n) {
+                        const float g = round_bf16(acc[i][j][q]);
+                        const float u = round_bf16(acc[i][j + NI / 2][q]);
+                        out[(size_t)r * p.ldo + c] = float_to_bf16_bits(silu(g) * u);
+                    }
+                }
+            } else if constexpr (EPI == kEpiStoreBf16) {
+                uint16_t* out = (uint16_t*)p.out;
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const int c = c0 + wn * TN + j * 32 + lcol;
+                    if (c < p.n) out[(size_t)r * p.ldo + c] = float_to_bf16_bits(acc[i][j][q]);
+                }
+            } else if constexpr (EPI == kEpiStoreF32) {
+                float* out = (float*)p.out;
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const int c = c0 + wn * TN + j * 32 + lcol;
+                    if (c < p.n) out[(size_t)r * p.ldo + c] = acc[i][j][q];
+                }
+            } else {  // kEpiScatterWeighted
+                const int slot = p.slots[r];
+                if (slot < 0 || slot >= p.assignments) continue;
+                const int t = slot / p.topk, rk = slot - t * p.topk;
+                const float wt = p.routes[(size_t)t * 2 * p.topk + p.topk + rk];
+                uint16_t* out = (uint16_t*)p.out;
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const int c = c0 + wn * TN + j * 32 + lcol;
+                    if (c < p.n) out[(size_t)slot * p.ldo + c] = float_to_bf16_bits(acc[i][j][q] * wt);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight-streaming MFMA kernel (decode / small groups), 16-row blocks
+// ---------------------------------------------------------------------------
+constexpr int kStreamWaves = 4;
+constexpr int kStreamUnroll = 4;  // K steps of 32 kept in flight per wave
+
+template <int AM, int EPI, bool Aligned>
+__global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm(GemmArgs p) {
+    constexpr bool kSilu = EPI == kEpiSilu;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (p.receipt && blockIdx.x == 0 && threadIdx.x == 0) {
+        p.receipt[0] = 16; p.receipt[1] = kSilu ? 32 : 16; p.receipt[2] = 32 * kStreamUnroll;
+        p.receipt[3] = kStreamWaves; p.receipt[4] = 1;
+    }
+    const int n_blocks = (p.n + 15) / 16;
+    const int live = live_blocks(p, 16);
+    const int total = live * n_blocks;
+    const int groups = (total + kStreamWaves - 1) / kStreamWaves;  // items per WG = 4 waves
+    const int per_xcd = (groups + kXcds - 1) / kXcds;
+    const int group = xcd_remap(blockIdx.x, per_xcd);
+    const int item = group * kStreamWaves + wave;
+    if (group >= groups || item >= total) return;
+    const int m_tile = item / n_blocks, nb = item - m_tile * n_blocks;
+    const int expert = p.tiles ? p.tiles[m_tile] : 0;
+    if (expert < 0) {
+        if constexpr (EPI == kEpiStoreBf16) {
+            uint16_t* out = (uint16_t*)p.out;
+            for (int i = lane; i < 256; i += 64) {
+                const int r = m_tile * 16 + i / 16, c = nb * 16 + i % 16;
+                if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
+            }
+        }
+        return;
+    }
+    const int row = m_tile * 16 + (lane & 15);
+    const int kofs = (lane >> 4) * 8;
+    // B operand: the 16 token rows of this block.
+    bool x_ok = row < p.rows;
+    long x_row = row;
+    if constexpr (AM == kAGather) {
+        const int slot = x_ok ? p.slots[row] : p.assignments;
+        x_ok = slot >= 0 && slot < p.assignments;
+        x_row = x_ok ? slot / p.topk : 0;
+    }
+    const uint16_t* xs = p.a + x_row * (long)p.lda;
+    // A operand: 16 weight rows (output columns); gate and up for SiLU.
+    const int wcol = nb * 16 + (lane & 15);
+    const bool w_ok = wcol < p.n;
+    const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
+    const uint16_t* wg = wexp + (long)(w_ok ? wcol : 0) * p.k;
+    const uint16_t* wu = kSilu ? wg + (long)p.w_up_offset * p.k : nullptr;
+
+    f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+    const int steps = (p.k + 31) / 32;
+    int s = 0;
+    for (; s + kStreamUnroll <= steps; s += kStreamUnroll) {
+        u32x4 g[kStreamUnroll], u[kStreamUnroll], x[kStreamUnroll];
+#pragma unroll
+        for (int q = 0; q < kStreamUnroll; ++q) {
+            const int kb = (s + q) * 32;
+            g[q] = load_chunk<Aligned>(wg, kb + kofs, p.k, w_ok);
+            if constexpr (kSilu) u[q] = load_chunk<Aligned>(wu, kb + kofs, p.k, w_ok);
+            x[q] = load_chunk<Aligned>(xs, kb + kofs, p.k, x_ok);
+        }
+#pragma unroll
+        for (int q = 0; q < kStreamUnroll; ++q) {
+            acc_g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(g[q]), as_bf16x8(x[q]), acc_g, 0, 0, 0);
+            if constexpr (kSilu)
+                acc_u = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(u[q]), as_bf16x8(x[q]), acc_u, 0, 0, 0);
+        }
+    }
+    for (; s < steps; ++s) {
+        const int kb = s * 32;
+        const u32x4 g = load_chunk<Aligned>(wg, kb + kofs, p.k, w_ok);
+        const u32x4 x = load_chunk<Aligned>(xs, kb + kofs, p.k, x_ok);
+        acc_g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(g), as_bf16x8(x), acc_g, 0, 0, 0);
+        if constexpr (kSilu) {
+            const u32x4 u = load_chunk<Aligned>(wu, kb + kofs, p.k, w_ok);
+            acc_u = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(u), as_bf16x8(x), acc_u, 0, 0, 0);
+        }
+    }
+
+    // 16x16 accumulator: value q of lane l is output column (l/16)*4 + q of the
+    // block (A rows) for token row l%16 (B columns).
+    const int orow = m_tile * 16 + (lane & 15);
+    if (orow >= p.rows) return;
+    const int oc = nb * 16 + (lane >> 4) * 4;
+    float v[4];
+    long out_row = orow;
+    if constexpr (EPI == kEpiSilu) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = silu(round_bf16(acc_g[q])) * round_bf16(acc_u[q]);
+    } else if constexpr (EPI == kEpiScatterWeighted) {
+        const int slot = p.slots[orow];
+        if (slot < 0 || slot >= p.assignments) return;
+        const int t = slot / p.topk, rk = slot - t * p.topk;
+        const float wt = p.routes[(size_t)t * 2 * p.topk + p.topk + rk];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc_g[q] * wt;
+        out_row = slot;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc_g[q];
+    }
+    if constexpr (EPI == kEpiStoreF32) {
+        float* out = (float*)p.out + out_row * (long)p.ldo;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (oc + q < p.n) out[oc + q] = v[q];
+    } else {
+        uint16_t* out = (uint16_t*)p.out + out_row * (long)p.ldo;
+        if (oc + 3 < p.n && (p.ldo % 4) == 0) {
+            u32x2 pk;
+            pk[0] = pack_bf16x2(v[0], v[1]);
+            pk[1] = pack_bf16x2(v[2], v[3]);
+            *(u32x2*)(out + oc) = pk;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (oc + q < p.n) out[oc + q] = float_to_bf16_bits(v[q]);
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int AM, int EPI>
+int launch_lds(const GemmArgs& p, bool aligned, hipStream_t s) {
+    constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
+    const long m_blocks = (p.rows + BM - 1) / BM;
+    const long n_tiles = (p.n + NOUT - 1) / NOUT;
+    const long total = m_blocks * n_tiles;
+    const long grid = (total + kXcds - 1) / kXcds * kXcds;
+    if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
+    if (aligned) lds_gemm<BM, BN, WM, WN, AM, EPI, true><<<(unsigned)grid, 64 * WM * WN, 0, s>>>(p);
+    else lds_gemm<BM, BN, WM, WN, AM, EPI, false><<<(unsigned)grid, 64 * WM * WN, 0, s>>>(p);
+    return (int)hipGetLastError();
+}
+
+template <int AM, int EPI>
+int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
+    const long m_blocks = (p.rows + 15) / 16;
+    const long n_blocks = (p.n + 15) / 16;
+    const long groups = (m_blocks * n_blocks + kStreamWaves - 1) / kStreamWaves;
+    const long grid = (groups + kXcds - 1) / kXcds * kXcds;
+    if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
+    if (aligned) stream_gemm<AM, EPI, true><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
+    else stream_gemm<AM, EPI, false><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
+    return (int)hipGetLastError();
+}
+
+template <int AM, int EPI>
+int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
+    switch (bm) {
+        case 16: return launch_stream<AM, EPI>(p, aligned, s);
+        case 32: return launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
+        case 64: return launch_lds<64, 128, 2, 2, AM, EPI>(p, aligned, s);
+        case 128: return launch_lds<128, 128, 2, 2, AM, EPI>(p, aligned, s);
+        default: return kInvalid;
+    }
+}
+
+}  // namespace
+
+// Row-block sizes of the compiled kernels: 16 (weight streaming) and
+// 32/64/128 (LDS-tiled MFMA).  Dispatch must pad experts to the same M.
+bool gemm_rows_supported(int bm) { return bm == 16 || bm == 32 || bm == 64 || bm == 128; }
+
+int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s) {
+    if (!p.a || !p.w || !p.out || p.rows <= 0 || p.n <= 0 || p.k <= 0 || p.lda < p.k || p.ldo < p.n)
+        return kInvalid;
+    if (!gemm_rows_supported(bm)) return kInvalid;
+    if ((a_mode == kAGather || epilogue == kEpiScatterWeighted) && (!p.slots || p.topk <= 0)) return kInvalid;
+    if (epilogue == kEpiScatterWeighted && !p.routes) return kInvalid;
+    const bool aligned = p.k % 8 == 0 && p.lda % 8 == 0 && ((uintptr_t)p.a % 16) == 0 && ((uintptr_t)p.w % 16) == 0 &&
+                         (p.w_expert_stride % 8) == 0;
+    if (a_mode == kAGather) {
+        switch (epilogue) {
+            case kEpiSilu: return launch_by_rows<kAGather, kEpiSilu>(p, bm, aligned, s);
+            case kEpiStoreBf16: return launch_by_rows<kAGather, kEpiStoreBf16>(p, bm, aligned, s);
+            default: return kInvalid;
+        }
+    }
+    switch (epilogue) {
+        case kEpiSilu: return launch_by_rows<kADirect, kEpiSilu>(p, bm, aligned, s);
+        case kEpiStoreBf16: return launch_by_rows<kADirect, kEpiStoreBf16>(p, bm, aligned, s);
+        case kEpiScatterWeighted: return launch_by_rows<kADirect, kEpiScatterWeighted>(p, bm, aligned, s);
+        case kEpiStoreF32: return launch_by_rows<kADirect, kEpiStoreF32>(p, bm, aligned, s);
+        default: return kInvalid;
+    }
+}
+
+}  // namespace tau_amd

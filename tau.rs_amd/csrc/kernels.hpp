@@ -1,0 +1,41 @@
+// Internal launcher interface shared by the library's translation units.
+#pragma once
+#include "common.hpp"
+
+namespace tau_amd {
+
+enum AMode { kAGather = 0, kADirect = 1 };
+enum Epilogue { kEpiSilu = 0, kEpiStoreBf16 = 1, kEpiScatterWeighted = 2, kEpiStoreF32 = 3 };
+
+struct GemmArgs {
+    const uint16_t* a;        // gather: x [T,lda]; direct: rows [rows,lda]
+    const uint16_t* w;        // expert weights [E][N_w][K] (N_w = 2I for gate_up)
+    const float* routes;      // [T, 2*topk] (scatter epilogue)
+    const int* slots;         // [cap] assignment per row (gather / scatter)
+    const int* tiles;         // [cap/BM] expert per row block, or null (single group)
+    const int* meta_total;    // padded row total on the device, or null
+    void* out;                // activated / projected / contributions / f32 output
+    int rows;                 // capacity (grouped) or row count (dense)
+    int assignments;          // T * topk; slot sentinel value
+    int topk;
+    int n;                    // output columns (I for gate_up-silu, N otherwise)
+    int k;                    // inner dimension
+    int lda;                  // A row stride (elements)
+    int ldo;                  // output row stride (elements)
+    long w_expert_stride;     // elements between experts
+    int w_up_offset;          // rows between gate row j and up row j (I)
+    int* receipt;             // optional 5 words stamped by the executed kernel
+};
+
+int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s);
+bool gemm_rows_supported(int bm);
+
+int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);
+int launch_routing(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
+                   hipStream_t s);
+int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,
+                    int* tiles, int tokens, int E, int K, int M, int capacity, hipStream_t s);
+int launch_combine(const void* contributions, void* output, const int* status, int tokens, int H, int K,
+                   hipStream_t s);
+
+}  // namespace tau_amd

@@ -1,0 +1,177 @@
+"""ctypes binding of libtau_moe_hip.so (declared in include/tau_moe.h).
+
+Torch is used only as device-memory and stream plumbing: every call passes raw
+device pointers and the current HIP stream to the C ABI.  The library must be
+built (``build.py``); loading fails loudly when it is missing, and there is no
+CPU or PyTorch fallback for any operation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtau_moe_hip.so")
+
+# Every symbol declared in include/tau_moe.h.
+EXPORTS = (
+    "tau_launch_moe_routing_fp32",
+    "tau_launch_moe_prefill_dispatch",
+    "tau_launch_moe_prefill_combine",
+    "tau_launch_moe_prefill_gemm",
+    "tau_launch_moe_prefill",
+    "tau_launch_silu_and_mul",
+    "tau_launch_moe_shared_combine",
+    "tau_launch_linear_bf16_fp32",
+    "tau_launch_moe_decode_gemm",
+    "tau_launch_fused_bf16_moe_decode",
+    "tau_moe_prefill_capacity",
+    "tau_moe_select_tile_rows",
+    "tau_moe_workspace_bytes",
+    "tau_launch_moe_routing_ex",
+    "tau_launch_moe_prefill_dispatch_ex",
+    "tau_launch_moe_prefill_combine_ex",
+    "tau_launch_moe_prefill_ex",
+    "tau_launch_moe_shared_expert_ex",
+    "tau_moe_build_target",
+)
+
+
+class TauGemmTile(ctypes.Structure):
+    _fields_ = [("m", ctypes.c_int), ("n", ctypes.c_int), ("k", ctypes.c_int),
+                ("warps", ctypes.c_int), ("stages", ctypes.c_int)]
+
+
+class TauDecodeProfile(ctypes.Structure):
+    _fields_ = [("backend", ctypes.c_int), ("n", ctypes.c_int), ("k", ctypes.c_int),
+                ("warps", ctypes.c_int), ("stages", ctypes.c_int)]
+
+
+class LaunchError(RuntimeError):
+    """Nonzero launch status (mirrors the reference's LaunchError{code,kernel})."""
+
+    def __init__(self, code: int, kernel: str):
+        super().__init__(f"{kernel} launch failed with status {code}")
+        self.code = code
+        self.kernel = kernel
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (no fallback exists)")
+    L = ctypes.CDLL(LIB_PATH)
+    p, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    sig = {
+        "tau_launch_moe_routing_fp32": [p, p, i, p],
+        "tau_launch_moe_prefill_dispatch": [p, p, p, p, p, i, i, i, p],
+        "tau_launch_moe_prefill_combine": [p, p, p, i, i, p],
+        "tau_launch_moe_prefill_gemm": [p, p, p, p, p, p, i, i, i, i, i, p, p, p],
+        "tau_launch_moe_prefill": [p] * 13 + [i] * 4 + [p, p, p, p],
+        "tau_launch_silu_and_mul": [p, p, i, i, i, p],
+        "tau_launch_moe_shared_combine": [p, p, p, p, p, i, i, p],
+        "tau_launch_linear_bf16_fp32": [p, p, p, i, i, i, p],
+        "tau_launch_moe_decode_gemm": [p, p, p, i, i, i, p, p, p],
+        "tau_launch_fused_bf16_moe_decode": [p] * 13 + [i] * 4 + [p, p, p, p],
+        "tau_moe_prefill_capacity": [i, i, i, i],
+        "tau_moe_select_tile_rows": [i, i, i, i, i],
+        "tau_moe_workspace_bytes": [i, i, i, i, i, i, p],
+        "tau_launch_moe_routing_ex": [p, i, p, i, i, i, p],
+        "tau_launch_moe_prefill_dispatch_ex": [p, i, p, p, p, p, p, i, i, i, i, i, p],
+        "tau_launch_moe_prefill_combine_ex": [p, p, p, i, i, i, i, p],
+        "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, p, p],
+        "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, p],
+    }
+    for name, args in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = i
+    L.tau_moe_prefill_capacity.restype = i64
+    L.tau_moe_build_target.argtypes = []
+    L.tau_moe_build_target.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def stream_ptr(stream=None):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def check(code: int, kernel: str) -> None:
+    if code != 0:
+        raise LaunchError(code, kernel)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return 0
+    if t.dtype == torch.bfloat16:
+        return 1
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def capacity(tokens: int, experts: int, top_k: int, tile_rows: int) -> int:
+    return int(lib().tau_moe_prefill_capacity(tokens, experts, top_k, tile_rows))
+
+
+def select_tile_rows(tokens, experts, top_k, hidden, intermediate) -> int:
+    return int(lib().tau_moe_select_tile_rows(tokens, experts, top_k, hidden, intermediate))
+
+
+def workspace_bytes(tokens, hidden, intermediate, experts, top_k, tile_rows):
+    out = (ctypes.c_size_t * 7)()
+    check(lib().tau_moe_workspace_bytes(tokens, hidden, intermediate, experts, top_k, tile_rows, out),
+          "workspace query")
+    return list(out)
+
+
+def routing_ex(logits, routes, experts, top_k, stream=None):
+    t = logits.shape[0]
+    check(lib().tau_launch_moe_routing_ex(ptr(logits), _dtype_code(logits), ptr(routes), t, experts, top_k,
+                                          stream_ptr(stream)), "MoE routing")
+
+
+def dispatch_ex(logits, routes, meta, offsets, slots, tiles, tokens, experts, top_k, tile_rows, cap,
+                stream=None):
+    code = lib().tau_launch_moe_prefill_dispatch_ex(
+        ptr(logits), _dtype_code(logits) if logits is not None else 0, ptr(routes), ptr(meta), ptr(offsets),
+        ptr(slots), ptr(tiles), tokens, experts, top_k, tile_rows, cap, stream_ptr(stream))
+    check(code, "MoE dispatch")
+
+
+def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, receipts=None, stream=None):
+    t, h = x.shape
+    i = down.shape[2]
+    code = lib().tau_launch_moe_prefill_ex(
+        ptr(x), ptr(logits), _dtype_code(logits), ptr(gate_up), ptr(down), ptr(ws["routes"]), ptr(ws["meta"]),
+        ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["activated"]),
+        ptr(ws["contributions"]), ptr(output), t, h, i, experts, top_k, tile_rows, ws["capacity"],
+        ptr(receipts), stream_ptr(stream))
+    check(code, "MoE grouped prefill")
+
+
+def shared_expert_ex(x, gate_up_s, down_s, gate_weight, routed, activated_ws, shared_ws, output, stream=None):
+    t, h = x.shape
+    i_s = down_s.shape[1]
+    code = lib().tau_launch_moe_shared_expert_ex(
+        ptr(x), ptr(gate_up_s), ptr(down_s), ptr(gate_weight), ptr(routed), ptr(activated_ws), ptr(shared_ws),
+        ptr(output), t, h, i_s, stream_ptr(stream))
+    check(code, "MoE shared expert")

@@ -1,0 +1,238 @@
+"""Host-side mirror of the reference's sparse-MoE operator interface.
+
+Names, argument meaning and error behaviour follow the reference's Rust owners
+(paths relative to the tau.rs root):
+
+* ``SparseMoeConfig.validate``  crates/models/src/components/sparse_moe/config.rs:52-78
+* ``MoePrefillTile``            crates/cuda-kernels/src/moe/config.rs:12-158 (parse,
+                                validate, ``values``, ``rows``)
+* ``moe_prefill_capacity``      crates/cuda-kernels/src/moe/prefill.rs:11-30
+* ``MoePrefillRunner``          crates/models/src/components/cuda/fused_moe/prefill.rs:
+                                workspace grown to the next power of two >= T
+                                (:330-340), ``calls()`` counter (:212-216),
+                                ``workspace_info`` and ``executed_tiles`` receipts
+* ``SparseMoeBlock.forward``    crates/models/src/components/sparse_moe.rs:102-151
+                                (routed experts, then the shared-expert combine)
+
+Every compute step runs in libtau_moe_hip.so; this module only validates,
+owns device workspaces (torch tensors as plumbing) and sequences launches.
+"""
+from __future__ import annotations
+
+import dataclasses
+from typing import Optional
+
+import torch
+
+from . import ffi
+
+
+@dataclasses.dataclass
+class SharedExpertConfig:
+    intermediate_size: int
+    gated: bool = True  # sigmoid(x . w_s) gate without bias
+
+
+@dataclasses.dataclass
+class SparseMoeConfig:
+    hidden_size: int
+    expert_intermediate_size: int
+    num_experts: int
+    experts_per_token: int
+    normalize_selected_weights: bool = True
+    shared_expert: Optional[SharedExpertConfig] = None
+
+    def validate(self) -> None:
+        """Raises ValueError with the reference's messages (config.rs:52-78)."""
+        if (self.hidden_size == 0 or self.expert_intermediate_size == 0 or self.num_experts == 0
+                or self.experts_per_token == 0):
+            raise ValueError("sparse MoE dimensions and expert counts must be non-zero")
+        if self.experts_per_token > self.num_experts:
+            raise ValueError("sparse MoE experts_per_token cannot exceed num_experts")
+        if self.shared_expert is not None and self.shared_expert.intermediate_size == 0:
+            raise ValueError("sparse MoE shared-expert intermediate size must be non-zero")
+        if not self.normalize_selected_weights:
+            raise ValueError("the HIP path implements normalised top-k weights only")
+        if self.num_experts > 1024 or self.experts_per_token > 32:
+            raise ValueError("the HIP path supports num_experts <= 1024 and experts_per_token <= 32")
+
+
+@dataclasses.dataclass(frozen=True)
+class MoePrefillTile:
+    """Five tile words M,N,K,warps,stages (config.rs:12-20).  M selects the CDNA4
+    row block (16 = weight-streaming kernel, 32/64/128 = LDS-tiled MFMA); the
+    remaining words are validated against the reference catalog."""
+    m: int = 16
+    n: int = 16
+    k: int = 16
+    warps: int = 1
+    stages: int = 1
+
+    def __post_init__(self):
+        ok = (self.m in (16, 32, 64, 128) and self.n in (16, 32, 64, 128) and self.k in (16, 32, 64, 128)
+              and self.warps in (1, 2, 4, 8) and self.stages in (1, 2))
+        if not ok:
+            raise ValueError(f"unsupported MoE prefill tile {self.values()}; expected M=16|32|64|128, "
+                             "N=16|32|64|128, K=16|32|64|128, warps=1|2|4|8, stages=1|2")
+
+    @classmethod
+    def parse(cls, text: str) -> "MoePrefillTile":
+        try:
+            vals = [int(v) for v in text.split(",")]
+        except ValueError:
+            raise ValueError("expected MoE prefill M,N,K,warps,stages") from None
+        if len(vals) != 5:
+            raise ValueError("expected five MoE prefill values: M,N,K,warps,stages")
+        return cls(*vals)
+
+    def values(self):
+        return [self.m, self.n, self.k, self.warps, self.stages]
+
+    def rows(self) -> int:
+        return self.m
+
+    def __str__(self):
+        return ",".join(str(v) for v in self.values())
+
+
+def moe_prefill_capacity(tokens: int, experts: int = 256, top_k: int = 8, tile_rows: int = 16) -> Optional[int]:
+    """None for invalid token counts, like the reference's Option (prefill.rs:17-30)."""
+    if tokens <= 0 or tokens > (1 << 20):
+        return None
+    c = ffi.capacity(tokens, experts, top_k, tile_rows)
+    return None if c < 0 else c
+
+
+def _next_pow2(n: int) -> int:
+    p = 1
+    while p < n:
+        p <<= 1
+    return p
+
+
+class MoePrefillRunner:
+    """Owns the routed-expert weights and the grouped-prefill workspaces."""
+
+    def __init__(self, config: SparseMoeConfig, gate_up: torch.Tensor, down: torch.Tensor,
+                 tile_rows: Optional[int] = None):
+        config.validate()
+        E, I, H = config.num_experts, config.expert_intermediate_size, config.hidden_size
+        if gate_up.shape != (E, 2 * I, H) or down.shape != (E, H, I):
+            raise ValueError("packed expert weights must be gate_up [E,2I,H] and down [E,H,I]")
+        if gate_up.dtype != torch.bfloat16 or down.dtype != torch.bfloat16 or not gate_up.is_cuda:
+            raise ValueError("the HIP path takes contiguous BF16 device weights")
+        self.config = config
+        self.gate_up = gate_up.contiguous()
+        self.down = down.contiguous()
+        self.fixed_tile_rows = tile_rows
+        self._ws = None
+        self._ws_key = None
+        self._calls = 0
+        self._receipts = torch.zeros(10, dtype=torch.int32, device=gate_up.device)
+
+    def calls(self) -> int:
+        return self._calls
+
+    def tile_rows_for(self, tokens: int) -> int:
+        c = self.config
+        if self.fixed_tile_rows:
+            return self.fixed_tile_rows
+        return ffi.select_tile_rows(tokens, c.num_experts, c.experts_per_token, c.hidden_size,
+                                    c.expert_intermediate_size)
+
+    def workspace(self, tokens: int, tile_rows: int):
+        """Workspaces sized for the next power of two >= tokens; reused while they fit."""
+        c = self.config
+        alloc_tokens = _next_pow2(tokens)
+        key = (tile_rows,)
+        if self._ws is not None and self._ws_key == key and self._ws["tokens"] >= tokens:
+            return self._ws
+        sizes = ffi.workspace_bytes(alloc_tokens, c.hidden_size, c.expert_intermediate_size, c.num_experts,
+                                    c.experts_per_token, tile_rows)
+        dev = self.gate_up.device
+        cap = ffi.capacity(alloc_tokens, c.num_experts, c.experts_per_token, tile_rows)
+        ws = {
+            "tokens": alloc_tokens,
+            "capacity": cap,
+            "routes": torch.empty(sizes[0] // 4, dtype=torch.float32, device=dev),
+            "meta": torch.empty(sizes[1] // 4, dtype=torch.int32, device=dev),
+            "offsets": torch.empty(sizes[2] // 4, dtype=torch.int32, device=dev),
+            "slots": torch.empty(sizes[3] // 4, dtype=torch.int32, device=dev),
+            "tiles": torch.empty(sizes[4] // 4, dtype=torch.int32, device=dev),
+            "activated": torch.empty(sizes[5] // 2, dtype=torch.bfloat16, device=dev),
+            "contributions": torch.empty(sizes[6] // 2, dtype=torch.bfloat16, device=dev),
+        }
+        self._ws, self._ws_key = ws, key
+        return ws
+
+    def workspace_info(self):
+        if self._ws is None:
+            return None
+        return (self._ws["tokens"], self._ws["capacity"], self._ws["slots"].data_ptr())
+
+    def executed_tiles(self):
+        return self._receipts.view(2, 5).tolist()
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor, out: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+        c = self.config
+        if x.dim() != 2 or x.shape[1] != c.hidden_size or x.dtype != torch.bfloat16:
+            raise ValueError("input must be BF16 [tokens, hidden]")
+        if logits.shape != (x.shape[0], c.num_experts):
+            raise ValueError("router logits must be [tokens, num_experts]")
+        tokens = x.shape[0]
+        tile_rows = self.tile_rows_for(tokens)
+        ws = self.workspace(tokens, tile_rows)
+        # Capacity of the allocation covers any token count up to ws["tokens"].
+        if out is None:
+            out = torch.empty_like(x)
+        ffi.prefill_ex(x.contiguous(), logits.contiguous(), self.gate_up, self.down, ws, out, c.num_experts,
+                       c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream)
+        self._calls += 1
+        return out
+
+    def plan_views(self, tokens: int):
+        """Device views of the last dispatch (routes [T,2K], meta, offsets, slots, tiles)."""
+        ws = self._ws
+        c = self.config
+        K, E = c.experts_per_token, c.num_experts
+        return {
+            "routes": ws["routes"][: tokens * 2 * K].view(tokens, 2 * K),
+            "meta": ws["meta"][: 2 * E + 2],
+            "offsets": ws["offsets"][: E + 1],
+            "slots": ws["slots"],
+            "tiles": ws["tiles"],
+        }
+
+
+class SparseMoeBlock:
+    """Routed experts plus the optional always-on shared expert."""
+
+    def __init__(self, config: SparseMoeConfig, gate_up, down, shared_gate_up=None, shared_down=None,
+                 shared_gate=None, tile_rows: Optional[int] = None):
+        self.runner = MoePrefillRunner(config, gate_up, down, tile_rows)
+        self.config = config
+        self.shared = None
+        if config.shared_expert is not None:
+            if shared_gate_up is None or shared_down is None:
+                raise ValueError("shared expert weights missing")
+            if config.shared_expert.gated and shared_gate is None:
+                raise ValueError("shared expert gate weight missing")
+            self.shared = (shared_gate_up.contiguous(), shared_down.contiguous(),
+                           shared_gate.contiguous() if config.shared_expert.gated else None)
+        self._shared_ws = None
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor, stream=None) -> torch.Tensor:
+        routed = self.runner.forward(x, logits, stream=stream)
+        if self.shared is None:
+            return routed
+        gu, dn, gw = self.shared
+        T = x.shape[0]
+        Is = self.config.shared_expert.intermediate_size
+        if self._shared_ws is None or self._shared_ws[0].shape[0] < T:
+            n = _next_pow2(T)
+            self._shared_ws = (torch.empty(n, Is, dtype=torch.bfloat16, device=x.device),
+                               torch.empty(n, x.shape[1], dtype=torch.bfloat16, device=x.device))
+        act, sh = self._shared_ws
+        ffi.shared_expert_ex(x, gu, dn, gw, routed, act[:T], sh[:T], routed, stream=stream)
+        return routed
