@@ -1,0 +1,234 @@
+"""MoE-layer throughput of the HIP path on one MI355X, with roofline and CPU baseline.
+
+A "step" is one pass of the routed expert FFN (routing, dispatch, gate_up +
+SiLU·mul, down + route weight, rank-ordered combine) over one batch of
+synthetic tokens already resident in HBM.  Default workload: the
+Qwen3-30B-A3B-shaped layer at batch-64 decode; weights
+rotate over several banks so the 256 MB MALL cannot hold the layer.
+
+Prints ONE JSON line.  `roofline` describes the dominant kernel of the step,
+timed with HIP events on the stream it runs on; `cpu_baseline` is the C
+restatement of the reference's f32 CPU path (the oracle) on a bounded token
+sample, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOADS = {
+    "c2": "c2_30b_a3b_decode",
+    "c3": "c3_30b_a3b_prefill",
+    "c4": "c4_next_sparse",
+    "c5p": "c5_235b_prefill",
+    "c5d": "c5_235b_decode",
+}
+
+
+def load_package():
+    if "tau_rs_amd" in sys.modules:
+        return sys.modules["tau_rs_amd"]
+    pkg = os.path.join(ROOT, "tau.rs_amd")
+    spec = importlib.util.spec_from_file_location("tau_rs_amd", os.path.join(pkg, "__init__.py"),
+                                                  submodule_search_locations=[pkg])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["tau_rs_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--banks", type=int, default=0, help="weight banks to rotate (0 = auto)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class Layer:
+    """One workload: inputs, rotating weight banks and a dispatch workspace."""
+
+    def __init__(self, tau, torch, shape, banks):
+        self.tau, self.torch, self.shape = tau, torch, shape
+        self.data = tau.inputs.make_layer(shape)
+        self.banks = [(self.data["gate_up"], self.data["down"])]
+        for _ in range(banks - 1):
+            self.banks.append((self.data["gate_up"].clone(), self.data["down"].clone()))
+        cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
+        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"])
+        self.tile_rows = self.runner.tile_rows_for(shape.tokens)
+        self.ws = self.runner.workspace(shape.tokens, self.tile_rows)
+        self.out = torch.empty_like(self.data["x"])
+        self.receipts = torch.zeros(10, dtype=torch.int32, device="cuda")
+
+    def step(self, i):
+        gu, dn = self.banks[i % len(self.banks)]
+        s = self.shape
+        self.tau.ffi.prefill_ex(self.data["x"], self.data["logits"], gu, dn, self.ws, self.out, s.experts,
+                                s.top_k, self.tile_rows, receipts=self.receipts)
+
+    def projection(self, i, which):
+        gu, dn = self.banks[i % len(self.banks)]
+        s = self.shape
+        if which == 0:
+            a, w, out = self.data["x"], gu, self.ws["activated"]
+        else:
+            a, w, out = self.ws["activated"], dn, self.ws["contributions"]
+        self.tau.ffi.grouped_gemm_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, s.experts, s.top_k,
+                                     self.tile_rows, which)
+
+
+def time_events(torch, fn, n):
+    """Average duration (ms) of n back-to-back launches, HIP events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(n):
+        fn(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / n
+
+
+def cpu_baseline(layer, seconds):
+    """Oracle f32 (restatement of the reference CPU path) on a token sample."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+
+    torch = layer.torch
+    s = layer.shape
+    sample = s.tokens if s.tokens <= 64 else 256
+    f = lambda t: t.float().cpu().numpy()
+    x = f(layer.data["x"][:sample])
+    lg = f(layer.data["logits"][:sample])
+    gu = f(layer.data["gate_up"])
+    dn = f(layer.data["down"])
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 25):
+        t0 = time.perf_counter()
+        ids, w = oracle.route(lg, s.top_k)
+        oracle.moe(x, ids, w, gu, dn)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+    return {
+        "value": sample / med,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample} of {s.tokens} tokens of {s.name}, f32 C restatement (oracle/moe_oracle.c), "
+                  f"median of {len(times) - 1} runs after 1 warm-up",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every GPU box in this build has one MI355X and the MoE layer is "
+              "benchmarked per GPU (expert-parallel sharding is a design note only); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    tau = load_package()
+    shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
+    weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
+    banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
+    layer = Layer(tau, torch, shape, banks)
+
+    for i in range(args.warmup):
+        layer.step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_step = time_events(torch, layer.step, args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # Routing facts for the algorithmic work.
+    meta = layer.ws["meta"][: 2 * shape.experts + 2].cpu()
+    counts = meta[: shape.experts]
+    distinct = int((counts > 0).sum())
+    status = int(meta[2 * shape.experts])
+    flops, bytes_ = tau.inputs.algorithmic_work(shape, distinct)
+
+    # Per-projection timing over the live dispatch.
+    n_proj = max(10, args.steps)
+    ms_gu = time_events(torch, lambda i: layer.projection(i, 0), n_proj)
+    ms_dn = time_events(torch, lambda i: layer.projection(i, 1), n_proj)
+    T, H, I, K = shape.tokens, shape.hidden, shape.intermediate, shape.top_k
+    A = T * K
+    decode = layer.tile_rows == 16
+    if decode:
+        gu_alg = distinct * 2 * I * H * 2 + T * H * 2 + A * I * 2
+        dn_alg = distinct * H * I * 2 + A * I * 2 + A * H * 2
+        gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e9, dn_alg / (ms_dn * 1e-3) / 1e9
+        unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
+        traffic_alg = (gu_alg, dn_alg)
+    else:
+        gu_alg, dn_alg = 2 * A * H * 2 * I, 2 * A * I * H
+        gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e12, dn_alg / (ms_dn * 1e-3) / 1e12
+        unit, peak, bound = "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "mfma"
+        traffic_alg = (gu_alg, dn_alg)
+    dominant = "gate_up" if ms_gu >= ms_dn else "down"
+    achieved = gu_rate if dominant == "gate_up" else dn_rate
+
+    tokens_per_s = T / (ms_step * 1e-3)
+    layer_hbm = bytes_ / (ms_step * 1e-3) / 1e9
+    layer_mfma = flops / (ms_step * 1e-3) / 1e12
+    result = {
+        "metric": "MoE-layer tokens/s; % bf16 MFMA peak (prefill), % HBM BW (decode)",
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; random router)",
+        "config": {
+            "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
+            "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
+            "distinct_experts": distinct, "plan_status": status,
+        },
+        "roofline": {
+            "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,
+            "frac": achieved / peak, "traffic": None,
+            "kernel_ms": {"gate_up": ms_gu, "down": ms_dn},
+            "algorithmic_per_launch": {"gate_up": traffic_alg[0], "down": traffic_alg[1]},
+        },
+        "layer_roofline": {
+            "hbm_GBs": layer_hbm, "hbm_frac": layer_hbm / HBM_PEAK_GBS,
+            "mfma_TFLOPs": layer_mfma, "mfma_frac": layer_mfma / MFMA_BF16_PEAK_TFLOPS,
+            "algorithmic_bytes": bytes_, "algorithmic_flops": flops,
+        },
+        "wall_s_timed": wall,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(layer, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -151,6 +151,17 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
                               int* receipts, void* stream);
 
+/* One grouped projection over an existing dispatch (meta/slots/tiles from
+ * tau_launch_moe_prefill_dispatch_ex with the same tile_rows):
+ * projection 0: a = input x [T,H], w = gate_up [E,2I,H], out = activated [cap,I]
+ *               (bf16(silu(bf16(g)) * bf16(u)));
+ * projection 1: a = activated [cap,I], w = down [E,H,I], out = contributions
+ *               [T*K,H] (bf16(acc * w_route) at each assignment's slot). */
+int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* routes, const int* slots,
+                                   const int* tiles, const int* meta, void* out, int tokens, int hidden,
+                                   int intermediate, int experts, int top_k, int tile_rows, int capacity,
+                                   int projection, int* receipt, void* stream);
+
 /* Always-on shared expert (shared_expert.rs:39-69): dense gated MLP over all
  * tokens with gate_up_s BF16 [2Is,H], down_s BF16 [Is,H]^T = [H,Is], then
  * output = bf16(fma(sigmoid(x . gate_weight), shared, routed)) (gate_weight

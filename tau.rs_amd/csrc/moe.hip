@@ -221,6 +221,26 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
     return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, s);
 }
 
+int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* routes, const int* slots,
+                                   const int* tiles, const int* meta, void* out, int tokens, int hidden,
+                                   int intermediate, int experts, int top_k, int tile_rows, int capacity,
+                                   int projection, int* receipt, void* stream) {
+    if (!a || !w || !routes || !slots || !tiles || !meta || !out ||
+        !shape_ok(tokens, hidden, intermediate, experts, top_k) || !gemm_rows_supported(tile_rows) ||
+        capacity < capacity_for(tokens, experts, top_k, tile_rows) || capacity % tile_rows ||
+        (projection != 0 && projection != 1))
+        return kInvalid;
+    const int* total = meta + 2 * experts + 1;
+    if (projection == 0) {
+        GemmArgs g = gate_up_args(a, w, routes, slots, tiles, total, out, tokens, top_k, capacity, hidden,
+                                  intermediate, receipt);
+        return launch_grouped_gemm(g, tile_rows, kAGather, kEpiSilu, as_stream(stream));
+    }
+    GemmArgs d = down_args(a, w, routes, slots, tiles, total, out, tokens, top_k, capacity, hidden, intermediate,
+                           receipt);
+    return launch_grouped_gemm(d, tile_rows, kADirect, kEpiScatterWeighted, as_stream(stream));
+}
+
 int tau_launch_moe_prefill(const void* input, const void* logits, const void* gate_up, const void* down,
                            float* routes, int* meta, int* offsets, int* slots, int* tiles, void* projected,
                            void* activated, void* contributions, void* output, int tokens, int hidden,

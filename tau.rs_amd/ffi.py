@@ -35,6 +35,7 @@ EXPORTS = (
     "tau_launch_moe_prefill_combine_ex",
     "tau_launch_moe_prefill_ex",
     "tau_launch_moe_shared_expert_ex",
+    "tau_launch_moe_grouped_gemm_ex",
     "tau_moe_build_target",
 )
 
@@ -88,6 +89,7 @@ def lib():
         "tau_launch_moe_prefill_combine_ex": [p, p, p, i, i, i, i, p],
         "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, p, p],
         "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, p],
+        "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 8 + [p, p],
     }
     for name, args in sig.items():
         fn = getattr(L, name)
@@ -175,3 +177,18 @@ def shared_expert_ex(x, gate_up_s, down_s, gate_weight, routed, activated_ws, sh
         ptr(x), ptr(gate_up_s), ptr(down_s), ptr(gate_weight), ptr(routed), ptr(activated_ws), ptr(shared_ws),
         ptr(output), t, h, i_s, stream_ptr(stream))
     check(code, "MoE shared expert")
+
+
+def grouped_gemm_ex(a, w, ws, out, tokens, hidden, intermediate, experts, top_k, tile_rows, projection,
+                    receipt=None, stream=None):
+    code = lib().tau_launch_moe_grouped_gemm_ex(
+        ptr(a), ptr(w), ptr(ws["routes"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["meta"]), ptr(out), tokens,
+        hidden, intermediate, experts, top_k, tile_rows, ws["capacity"], projection, ptr(receipt),
+        stream_ptr(stream))
+    check(code, "MoE grouped GEMM")
+
+
+def combine_ex(contributions, output, meta, tokens, hidden, experts, top_k, stream=None):
+    code = lib().tau_launch_moe_prefill_combine_ex(ptr(contributions), ptr(output), ptr(meta), tokens, hidden,
+                                                   experts, top_k, stream_ptr(stream))
+    check(code, "MoE combine")
