@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--banks", type=int, default=0, help="weight banks to rotate (0 = auto)")
+    ap.add_argument("--tile-rows", type=int, default=0, help="override the library's row-block choice")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
@@ -63,14 +64,14 @@ def parse():
 class Layer:
     """One workload: inputs, rotating weight banks and a dispatch workspace."""
 
-    def __init__(self, tau, torch, shape, banks):
+    def __init__(self, tau, torch, shape, banks, tile_rows=0):
         self.tau, self.torch, self.shape = tau, torch, shape
         self.data = tau.inputs.make_layer(shape)
         self.banks = [(self.data["gate_up"], self.data["down"])]
         for _ in range(banks - 1):
             self.banks.append((self.data["gate_up"].clone(), self.data["down"].clone()))
         cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
-        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"])
+        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"], tile_rows=tile_rows or None)
         self.tile_rows = self.runner.tile_rows_for(shape.tokens)
         self.ws = self.runner.workspace(shape.tokens, self.tile_rows)
         self.out = torch.empty_like(self.data["x"])
@@ -152,7 +153,7 @@ def main():
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
-    layer = Layer(tau, torch, shape, banks)
+    layer = Layer(tau, torch, shape, banks, args.tile_rows)
 
     for i in range(args.warmup):
         layer.step(i)
@@ -175,7 +176,7 @@ def main():
     ms_dn = time_events(torch, lambda i: layer.projection(i, 1), n_proj)
     T, H, I, K = shape.tokens, shape.hidden, shape.intermediate, shape.top_k
     A = T * K
-    decode = layer.tile_rows == 16
+    decode = layer.tile_rows <= 32
     if decode:
         gu_alg = distinct * 2 * I * H * 2 + T * H * 2 + A * I * 2
         dn_alg = distinct * H * I * 2 + A * I * 2 + A * H * 2
@@ -209,7 +210,7 @@ def main():
         "config": {
             "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
-            "distinct_experts": distinct, "plan_status": status,
+            "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
         "roofline": {
             "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,

@@ -113,7 +113,7 @@ int tau_launch_fused_bf16_moe_decode(const void* input, const void* logits, cons
                                      const TauDecodeProfile* gate_up_config, const TauDecodeProfile* down_config,
                                      int* receipts, void* stream);
 
-/* ---------------- generalised entry points (any E <= 1024, K <= 32) ---------------- */
+/* ---------------- generalised entry points (any E <= 512, K <= 32) ---------------- */
 
 /* Capacity of the padded dispatch, generalising moe_prefill_capacity_for_tile
  * (crates/cuda-kernels/src/moe/prefill.rs:17-30); -1 for invalid input. */

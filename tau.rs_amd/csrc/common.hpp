@@ -57,8 +57,11 @@ __device__ __forceinline__ float sigmoid(float v) {
 
 // Block-index remap so that consecutive work items land on the same XCD
 // (block b runs on XCD b % 8).  `per_xcd` = ceil(total / 8); returns an item
-// index in [0, 8 * per_xcd); callers drop indices >= total.
+// index in [0, 8 * per_xcd), or -1 for blocks past 8 * per_xcd (grids are
+// sized from capacity, so the tail blocks must not alias live items).
+// Callers also drop indices >= total.
 __device__ __forceinline__ int xcd_remap(int block, int per_xcd) {
+    if (block >= kXcds * per_xcd) return -1;
     return (block % kXcds) * per_xcd + block / kXcds;
 }
 

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * WM * WN) void lds_gemm(GemmArgs p) {
     const int total = live * n_tiles;
     const int per_xcd = (total + kXcds - 1) / kXcds;
     const int item = xcd_remap(blockIdx.x, per_xcd);
-    if (item >= total) return;
+    if (item < 0 || item >= total) return;
     const int m_tile = item / n_tiles, n_tile = item - m_tile * n_tiles;
     const int expert = p.tiles ? p.tiles[m_tile] : 0;
     const int row0 = m_tile * BM;
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm(GemmArgs p) {
     const int per_xcd = (groups + kXcds - 1) / kXcds;
     const int group = xcd_remap(blockIdx.x, per_xcd);
     const int item = group * kStreamWaves + wave;
-    if (group >= groups || item >= total) return;
+    if (group < 0 || group >= groups || item >= total) return;
     const int m_tile = item / n_blocks, nb = item - m_tile * n_blocks;
     const int expert = p.tiles ? p.tiles[m_tile] : 0;
     if (expert < 0) {
@@ -386,6 +386,198 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm(GemmArgs p) {
     }
 }
 
+// Pipelined weight-streaming kernel for 16-byte-aligned operands.  Each wave
+// owns NB 16-column blocks (gate and up blocks for SiLU) of one 16-row block;
+// loads carry no branches (invalid rows are clamped to a valid address and
+// zeroed afterwards) and batches of U K-steps are double-buffered, so one
+// batch is in flight while the previous one feeds the MFMAs.
+template <int NB, int U, int RT>
+struct StreamBatch {
+    u32x4 x[RT][U];
+    u32x4 g[NB][U];
+    u32x4 u[NB][U];
+};
+
+// RT 16-row token groups share every weight fragment (rows per item = 16*RT).
+template <int AM, int EPI, int NB, int U, int W, int RT>
+__global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
+    constexpr bool kSilu = EPI == kEpiSilu;
+    constexpr int R = 16 * RT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (p.receipt && blockIdx.x == 0 && threadIdx.x == 0) {
+        p.receipt[0] = R; p.receipt[1] = 16 * NB * (kSilu ? 2 : 1); p.receipt[2] = 32 * U;
+        p.receipt[3] = W; p.receipt[4] = 2;
+    }
+    const int n_groups = (p.n + 16 * NB - 1) / (16 * NB);
+    const int live = live_blocks(p, R);
+    const int total = live * n_groups;
+    const int groups = (total + W - 1) / W;
+    const int per_xcd = (groups + kXcds - 1) / kXcds;
+    const int group = xcd_remap(blockIdx.x, per_xcd);
+    const int item = group * W + wave;
+    if (group < 0 || group >= groups || item >= total) return;
+    const int m_tile = item / n_groups, ng = item - m_tile * n_groups;
+    const int expert = p.tiles ? p.tiles[m_tile] : 0;
+    if (expert < 0) {
+        if constexpr (EPI == kEpiStoreBf16) {
+            uint16_t* out = (uint16_t*)p.out;
+            for (int i = lane; i < R * 16 * NB; i += 64) {
+                const int r = m_tile * R + i / (16 * NB), c = ng * 16 * NB + i % (16 * NB);
+                if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
+            }
+        }
+        return;
+    }
+    const int kofs = (lane >> 4) * 8;
+    bool x_ok[RT];
+    const uint16_t* xs[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int row = m_tile * R + rt * 16 + (lane & 15);
+        bool ok = row < p.rows;
+        long x_row = ok ? row : 0;
+        if constexpr (AM == kAGather) {
+            const int slot = ok ? p.slots[row] : p.assignments;
+            ok = slot >= 0 && slot < p.assignments;
+            x_row = ok ? slot / p.topk : 0;
+        }
+        x_ok[rt] = ok;
+        xs[rt] = p.a + x_row * (long)p.lda + kofs;
+    }
+    const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
+    const uint16_t* wg[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int col = ng * 16 * NB + b * 16 + (lane & 15);
+        wg[b] = wexp + (long)(col < p.n ? col : 0) * p.k + kofs;
+    }
+    const long up = (long)p.w_up_offset * p.k;
+
+    f32x4 acc_g[NB][RT], acc_u[NB][RT];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc_g[b][rt][q] = acc_u[b][rt][q] = 0.f;
+
+    auto load = [&](StreamBatch<NB, U, RT>& t, int kb) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                t.g[b][q] = *(const u32x4*)(wg[b] + kb + q * 32);
+                if constexpr (kSilu) t.u[b][q] = *(const u32x4*)(wg[b] + up + kb + q * 32);
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) t.x[rt][q] = *(const u32x4*)(xs[rt] + kb + q * 32);
+        }
+    };
+    auto mma = [&](StreamBatch<NB, U, RT>& t) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                u32x4 xv = t.x[rt][q];
+                if (!x_ok[rt]) xv = u32x4{0u, 0u, 0u, 0u};
+                const bf16x8 xb = as_bf16x8(xv);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    acc_g[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(t.g[b][q]), xb, acc_g[b][rt], 0, 0, 0);
+                    if constexpr (kSilu)
+                        acc_u[b][rt] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(t.u[b][q]), xb, acc_u[b][rt], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    constexpr int KB = 32 * U;
+    const int main_k = p.k / KB * KB;
+    StreamBatch<NB, U, RT> b0, b1;
+    int kb = 0;
+    if (main_k > 0) {
+        load(b0, 0);
+        for (; kb + 2 * KB <= main_k; kb += 2 * KB) {
+            load(b1, kb + KB);
+            mma(b0);
+            if (kb + 2 * KB < main_k) load(b0, kb + 2 * KB);
+            mma(b1);
+        }
+        if (kb < main_k) {  // one batch left (already loaded into b0)
+            mma(b0);
+            kb += KB;
+        }
+    }
+    // Tail (K not a multiple of 32*U): 8-element chunks, masked.
+    for (; kb < p.k; kb += 32) {
+        const bool in = kb + kofs < p.k;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            u32x4 xv = {0u, 0u, 0u, 0u};
+            if (in && x_ok[rt]) xv = *(const u32x4*)(xs[rt] + kb);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                u32x4 gv = {0u, 0u, 0u, 0u}, uv = {0u, 0u, 0u, 0u};
+                if (in) {
+                    gv = *(const u32x4*)(wg[b] + kb);
+                    if constexpr (kSilu) uv = *(const u32x4*)(wg[b] + up + kb);
+                }
+                acc_g[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(gv), as_bf16x8(xv), acc_g[b][rt], 0, 0, 0);
+                if constexpr (kSilu)
+                    acc_u[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(uv), as_bf16x8(xv), acc_u[b][rt], 0, 0, 0);
+            }
+        }
+    }
+
+    // 16x16 accumulator: value q of lane l is column (l/16)*4 + q of the block,
+    // token row l%16 of its group.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int orow = m_tile * R + rt * 16 + (lane & 15);
+        if (orow >= p.rows) continue;
+        long out_row = orow;
+        float wt = 1.0f;
+        if constexpr (EPI == kEpiScatterWeighted) {
+            const int slot = p.slots[orow];
+            if (slot < 0 || slot >= p.assignments) continue;
+            const int t = slot / p.topk, rk = slot - t * p.topk;
+            wt = p.routes[(size_t)t * 2 * p.topk + p.topk + rk];
+            out_row = slot;
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int oc = ng * 16 * NB + b * 16 + (lane >> 4) * 4;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (EPI == kEpiSilu)
+                    v[q] = silu(round_bf16(acc_g[b][rt][q])) * round_bf16(acc_u[b][rt][q]);
+                else if constexpr (EPI == kEpiScatterWeighted) v[q] = acc_g[b][rt][q] * wt;
+                else v[q] = acc_g[b][rt][q];
+            }
+            if constexpr (EPI == kEpiStoreF32) {
+                float* out = (float*)p.out + out_row * (long)p.ldo;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (oc + q < p.n) out[oc + q] = v[q];
+            } else {
+                uint16_t* out = (uint16_t*)p.out + out_row * (long)p.ldo;
+                if (oc + 3 < p.n && (p.ldo % 4) == 0) {
+                    u32x2 pk;
+                    pk[0] = pack_bf16x2(v[0], v[1]);
+                    pk[1] = pack_bf16x2(v[2], v[3]);
+                    *(u32x2*)(out + oc) = pk;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (oc + q < p.n) out[oc + q] = float_to_bf16_bits(v[q]);
+                }
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int AM, int EPI>
 int launch_lds(const GemmArgs& p, bool aligned, hipStream_t s) {
     constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
@@ -399,23 +591,36 @@ int launch_lds(const GemmArgs& p, bool aligned, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
-template <int AM, int EPI>
+// Weight-streaming launch.  Columns per wave (NB blocks of 16) and K steps per
+// batch (U) were chosen by measurement on MI355X: SiLU gate_up streams two
+// weight rows per output column and prefers NB=1; single-stream projections
+// prefer NB=4.
+template <int AM, int EPI, int RT>
 int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
-    const long m_blocks = (p.rows + 15) / 16;
-    const long n_blocks = (p.n + 15) / 16;
+    constexpr int NB = EPI == kEpiSilu ? 1 : 4, U = 4;
+    const int rows = 16 * RT;
+    const long m_blocks = (p.rows + rows - 1) / rows;
+    if (!aligned) {
+        if (RT != 1) return kInvalid;
+        const long n_blocks = (p.n + 15) / 16;
+        const long groups = (m_blocks * n_blocks + kStreamWaves - 1) / kStreamWaves;
+        const long grid = (groups + kXcds - 1) / kXcds * kXcds;
+        stream_gemm<AM, EPI, false><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
+        return (int)hipGetLastError();
+    }
+    const long n_blocks = (p.n + 16 * NB - 1) / (16 * NB);
     const long groups = (m_blocks * n_blocks + kStreamWaves - 1) / kStreamWaves;
     const long grid = (groups + kXcds - 1) / kXcds * kXcds;
     if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
-    if (aligned) stream_gemm<AM, EPI, true><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
-    else stream_gemm<AM, EPI, false><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
+    stream_gemm_fast<AM, EPI, NB, U, kStreamWaves, RT><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
     return (int)hipGetLastError();
 }
 
 template <int AM, int EPI>
 int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
     switch (bm) {
-        case 16: return launch_stream<AM, EPI>(p, aligned, s);
-        case 32: return launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
+        case 16: return launch_stream<AM, EPI, 1>(p, aligned, s);
+        case 32: return aligned ? launch_stream<AM, EPI, 2>(p, aligned, s) : launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
         case 64: return launch_lds<64, 128, 2, 2, AM, EPI>(p, aligned, s);
         case 128: return launch_lds<128, 128, 2, 2, AM, EPI>(p, aligned, s);
         default: return kInvalid;

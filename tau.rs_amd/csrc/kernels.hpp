@@ -34,7 +34,8 @@ int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);
 int launch_routing(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                    hipStream_t s);
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,
-                    int* tiles, int tokens, int E, int K, int M, int capacity, hipStream_t s);
+                    int* tiles, int tokens, int E, int K, int M, int capacity, void* scratch, size_t scratch_bytes,
+                    hipStream_t s);
 int launch_combine(const void* contributions, void* output, const int* status, int tokens, int H, int K,
                    hipStream_t s);
 

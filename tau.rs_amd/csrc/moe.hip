@@ -87,7 +87,7 @@ GemmArgs down_args(const void* activated, const void* down, const float* routes,
 
 bool shape_ok(int tokens, int hidden, int intermediate, int experts, int top_k) {
     return tokens > 0 && tokens <= kMaxTokens && hidden > 0 && intermediate > 0 && intermediate <= INT_MAX / 2 &&
-           experts > 0 && experts <= 1024 && top_k > 0 && top_k <= 32 && top_k <= experts &&
+           experts > 0 && experts <= 512 && top_k > 0 && top_k <= 32 && top_k <= experts &&
            (int64_t)tokens * top_k * hidden <= (int64_t)1 << 40;
 }
 
@@ -145,7 +145,7 @@ int tau_launch_moe_prefill_dispatch_ex(const void* logits, int logits_dtype, flo
                                        int tile_rows, int capacity, void* stream) {
     if (tokens <= 0 || tokens > kMaxTokens || !gemm_rows_supported(tile_rows)) return kInvalid;
     return launch_dispatch(logits, logits_dtype, routes, meta, offsets, slots, tiles, tokens, experts, top_k,
-                           tile_rows, capacity, as_stream(stream));
+                           tile_rows, capacity, nullptr, 0, as_stream(stream));
 }
 
 int tau_launch_moe_prefill_dispatch(const float* routes, int* meta, int* offsets, int* slots, int* tiles,
@@ -206,8 +206,10 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
         capacity % tile_rows)
         return kInvalid;
     hipStream_t s = as_stream(stream);
+    // The contributions buffer is free until the down projection: it holds the
+    // multi-workgroup dispatch's per-chunk counts.
     int code = launch_dispatch(logits, logits_dtype, routes, meta, offsets, slots, tiles, tokens, experts, top_k,
-                               tile_rows, capacity, s);
+                               tile_rows, capacity, contributions, (size_t)2 * tokens * top_k * hidden, s);
     if (code) return code;
     const int* total = meta + 2 * experts + 1;
     GemmArgs g = gate_up_args(input, gate_up, routes, slots, tiles, total, activated, tokens, top_k, capacity,

@@ -27,25 +27,62 @@ __device__ __forceinline__ uint32_t orderable(float v) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        uint64_t o = __shfl_xor(v, d, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+// Wave-wide reductions built from DPP lane moves (no LDS traffic): butterfly
+// inside each 16-lane row, then row_bcast:15 / row_bcast:31 carry the row
+// results upward so lane 63 holds the full reduction, read back uniformly.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t identity, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, Ctrl, RowMask, 0xf, false);
 }
 
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ float dpp_f32(float identity, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), Ctrl, RowMask,
+                                                      0xf, false));
+}
+
+constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kRowHalfMirror = 0x141, kRowMirror = 0x140;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
-    return v;
+    const float id = -INFINITY;
+    v = fmaxf(v, dpp_f32<kQuadXor1, 0xf>(id, v));
+    v = fmaxf(v, dpp_f32<kQuadXor2, 0xf>(id, v));
+    v = fmaxf(v, dpp_f32<kRowHalfMirror, 0xf>(id, v));
+    v = fmaxf(v, dpp_f32<kRowMirror, 0xf>(id, v));
+    v = fmaxf(v, dpp_f32<kRowBcast15, 0xa>(id, v));
+    v = fmaxf(v, dpp_f32<kRowBcast31, 0xc>(id, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
+    v += dpp_f32<kQuadXor1, 0xf>(0.f, v);
+    v += dpp_f32<kQuadXor2, 0xf>(0.f, v);
+    v += dpp_f32<kRowHalfMirror, 0xf>(0.f, v);
+    v += dpp_f32<kRowMirror, 0xf>(0.f, v);
+    v += dpp_f32<kRowBcast15, 0xa>(0.f, v);
+    v += dpp_f32<kRowBcast31, 0xc>(0.f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint64_t max_step_u64(uint64_t v) {
+    const uint32_t lo = dpp_u32<Ctrl, RowMask>(0u, (uint32_t)v);
+    const uint32_t hi = dpp_u32<Ctrl, RowMask>(0u, (uint32_t)(v >> 32));
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_step_u64<kQuadXor1, 0xf>(v);
+    v = max_step_u64<kQuadXor2, 0xf>(v);
+    v = max_step_u64<kRowHalfMirror, 0xf>(v);
+    v = max_step_u64<kRowMirror, 0xf>(v);
+    v = max_step_u64<kRowBcast15, 0xa>(v);
+    v = max_step_u64<kRowBcast31, 0xc>(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 template <typename T>
@@ -113,7 +150,7 @@ __device__ __forceinline__ void route_token(const T* row, float* out, int E, int
 #pragma unroll
         for (int j = 0; j < EP; ++j)
             if (j == slot) mine = p[j];
-        const float prob = __shfl(mine, owner, 64);
+        const float prob = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), owner));
         if (lane == owner) taken |= 1u << slot;
         selected_sum += prob;  // rank order, as routing.rs:187-191
         if (lane == r) { my_id = id; my_weight = prob; }
@@ -147,7 +184,8 @@ __device__ __forceinline__ int assignment_expert(const float* routes, int a, int
     const float id = row[r], w = row[K + r];
     bool valid = __builtin_isfinite(id) && id >= 0.f && id < (float)E && floorf(id) == id &&
                  __builtin_isfinite(w) && w >= 0.f;
-    for (int q = 0; q < r && valid; ++q) valid = row[q] != id;
+    // No short-circuit: the earlier-rank loads are independent and issue together.
+    for (int q = 0; q < r; ++q) valid &= row[q] != id;
     return valid ? (int)id : -1;
 }
 
@@ -171,42 +209,43 @@ struct DispatchArgs {
     int* offsets;
     int* slots;
     int* tiles;
+    int* scratch;  // multi-workgroup: [chunks][E] counts, then bases; [chunks] flags
     int tokens, E, K, M;
     int capacity;
     int expert_bits;
+    int chunk;     // assignments per workgroup chunk (multiple of 1024)
 };
 
-// One workgroup builds counts, padded offsets, the stable permutation, the
-// tile worklist and the status/padded-total words.  With `Fused`, the same
-// workgroup first routes every token (used for decode-sized batches).
-template <bool Fused, int EP>
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs p) {
-    extern __shared__ int lds[];
-    int* wcount = lds;                                  // [16][E]
-    int* total = lds + kDispatchWaves * p.E;             // [E]
-    int* padded = total + p.E;                          // [E + 1] exclusive scan
-    int* flag = padded + p.E + 1;                       // [1]
-    int* scan_tmp = flag + 1;                           // [kDispatchThreads]
+struct DispatchLds {
+    int* wcount;    // [16][E] per-wave counts, then per-wave bases
+    int* total;     // [E] counts of this workgroup's span
+    int* padded;    // [E + 1] padded exclusive scan
+    int* flag;      // [1]
+    int* scan_tmp;  // [kDispatchThreads]
+};
+
+__device__ __forceinline__ DispatchLds dispatch_lds(int* lds, int E) {
+    DispatchLds l;
+    l.wcount = lds;
+    l.total = lds + kDispatchWaves * E;
+    l.padded = l.total + E;
+    l.flag = l.padded + E + 1;
+    l.scan_tmp = l.flag + 1;
+    return l;
+}
+
+// Per-wave counts of [span_begin, span_end), each wave a contiguous segment;
+// then per-expert exclusive prefix over waves (wcount becomes per-wave bases)
+// and total[e] = count of e in the span.  Sets flag on any invalid route.
+__device__ void span_counts(const DispatchArgs& p, const DispatchLds& l, int span_begin, int span_end) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int A = p.tokens * p.K;
-
-    if constexpr (Fused) {
-        for (int t = wave; t < p.tokens; t += kDispatchWaves) {
-            if (p.logits_bf16)
-                route_token<EP, uint16_t>(p.logits_bf16 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
-            else
-                route_token<EP, float>(p.logits_f32 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
-        }
-        __threadfence_block();
-    }
-    for (int i = tid; i < kDispatchWaves * p.E; i += kDispatchThreads) wcount[i] = 0;
-    if (tid == 0) flag[0] = 0;
+    for (int i = tid; i < kDispatchWaves * p.E; i += kDispatchThreads) l.wcount[i] = 0;
+    if (tid == 0) l.flag[0] = 0;
     __syncthreads();
-
-    // Phase 1: per-wave counts over contiguous segments.
-    const int seg = ((A + kDispatchWaves - 1) / kDispatchWaves + 63) / 64 * 64;
-    const int begin = wave * seg, end = min(A, begin + seg);
-    int* my = wcount + wave * p.E;
+    const int n = span_end - span_begin;
+    const int seg = ((n + kDispatchWaves - 1) / kDispatchWaves + 63) / 64 * 64;
+    const int begin = span_begin + wave * seg, end = min(span_end, begin + seg);
+    int* my = l.wcount + wave * p.E;
     bool bad = false;
     for (int a0 = begin; a0 < end; a0 += 64) {
         const int a = a0 + lane;
@@ -219,45 +258,28 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
         const uint64_t peers = match_expert(e, active, p.expert_bits);
         if (active && (peers & lanemask_lt()) == 0) my[e] += __popcll(peers);
     }
-    if (__any(bad) && lane == 0) flag[0] = 1;
+    if (__any(bad) && lane == 0) l.flag[0] = 1;
     __syncthreads();
-
-    // Phase 2: per-expert prefix over waves, then padded exclusive scan over experts.
     for (int e = tid; e < p.E; e += kDispatchThreads) {
         int run = 0;
         for (int w = 0; w < kDispatchWaves; ++w) {
-            const int c = wcount[w * p.E + e];
-            wcount[w * p.E + e] = run;
+            const int c = l.wcount[w * p.E + e];
+            l.wcount[w * p.E + e] = run;
             run += c;
         }
-        total[e] = run;
+        l.total[e] = run;
     }
     __syncthreads();
-    {
-        // Each thread owns a contiguous run of experts, then a block scan.
-        const int per = (p.E + kDispatchThreads - 1) / kDispatchThreads;
-        const int e0 = tid * per;
-        int local = 0;
-        for (int e = e0; e < min(p.E, e0 + per); ++e) local += (total[e] + p.M - 1) / p.M * p.M;
-        scan_tmp[tid] = local;
-        __syncthreads();
-        for (int d = 1; d < kDispatchThreads; d <<= 1) {
-            const int v = tid >= d ? scan_tmp[tid - d] : 0;
-            __syncthreads();
-            scan_tmp[tid] += v;
-            __syncthreads();
-        }
-        int run = scan_tmp[tid] - local;
-        for (int e = e0; e < min(p.E, e0 + per); ++e) {
-            padded[e] = run;
-            run += (total[e] + p.M - 1) / p.M * p.M;
-        }
-        if (tid == kDispatchThreads - 1) padded[p.E] = scan_tmp[tid];
-    }
-    __syncthreads();
+}
 
-    // Phase 3: stable scatter.  Wave w's cursor for expert e starts at
-    // offsets[e] + (assignments of e in earlier segments).
+// Stable scatter of the span: slot position = base[e] + per-wave base + in-wave rank.
+__device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int span_begin, int span_end,
+                             const int* base /* [E], LDS or global */) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = span_end - span_begin;
+    const int seg = ((n + kDispatchWaves - 1) / kDispatchWaves + 63) / 64 * 64;
+    const int begin = span_begin + wave * seg, end = min(span_end, begin + seg);
+    int* my = l.wcount + wave * p.E;
     for (int a0 = begin; a0 < end; a0 += 64) {
         const int a = a0 + lane;
         int e = -1;
@@ -265,26 +287,54 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
         const bool active = e >= 0;
         const uint64_t peers = match_expert(e, active, p.expert_bits);
         const int leader = peers ? __ffsll((unsigned long long)peers) - 1 : 0;
-        int base = 0;
-        if (active && lane == leader) base = my[e];
-        base = __shfl(base, leader, 64);
+        int off = 0;
+        if (active && lane == leader) off = my[e];
+        off = __shfl(off, leader, 64);
         if (active) {
             const int rank = __popcll(peers & lanemask_lt());
-            p.slots[padded[e] + base + rank] = a;
-            if (lane == leader) my[e] = base + __popcll(peers);
+            p.slots[base[e] + off + rank] = a;
+            if (lane == leader) my[e] = off + __popcll(peers);
         }
     }
+}
 
-    // Phase 4: metadata, tile worklist and padding sentinels.
-    const int padded_total = padded[p.E];
+// Padded exclusive scan of total[] over experts into padded[0..E].
+__device__ void padded_scan(const DispatchArgs& p, const DispatchLds& l) {
+    const int tid = threadIdx.x;
+    const int per = (p.E + kDispatchThreads - 1) / kDispatchThreads;
+    const int e0 = tid * per;
+    int local = 0;
+    for (int e = e0; e < min(p.E, e0 + per); ++e) local += (l.total[e] + p.M - 1) / p.M * p.M;
+    l.scan_tmp[tid] = local;
+    __syncthreads();
+    for (int d = 1; d < kDispatchThreads; d <<= 1) {
+        const int v = tid >= d ? l.scan_tmp[tid - d] : 0;
+        __syncthreads();
+        l.scan_tmp[tid] += v;
+        __syncthreads();
+    }
+    int run = l.scan_tmp[tid] - local;
+    for (int e = e0; e < min(p.E, e0 + per); ++e) {
+        l.padded[e] = run;
+        run += (l.total[e] + p.M - 1) / p.M * p.M;
+    }
+    if (tid == kDispatchThreads - 1) l.padded[p.E] = l.scan_tmp[tid];
+    __syncthreads();
+}
+
+// Metadata words, offsets, the tile worklist and padding sentinels.
+__device__ void finalize_plan(const DispatchArgs& p, const DispatchLds& l, int status) {
+    const int tid = threadIdx.x;
+    const int A = p.tokens * p.K;
+    const int padded_total = l.padded[p.E];
     for (int e = tid; e < p.E; e += kDispatchThreads) {
-        p.meta[e] = total[e];
-        p.meta[p.E + e] = total[e];
-        p.offsets[e] = padded[e];
+        p.meta[e] = l.total[e];
+        p.meta[p.E + e] = l.total[e];
+        p.offsets[e] = l.padded[e];
     }
     if (tid == 0) {
         p.offsets[p.E] = padded_total;
-        p.meta[2 * p.E] = flag[0];
+        p.meta[2 * p.E] = status;
         p.meta[2 * p.E + 1] = padded_total;
     }
     const int ntiles = p.capacity / p.M;
@@ -295,14 +345,87 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
             int lo = 0, hi = p.E - 1;  // last expert with padded[e] <= row0
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
-                if (padded[mid] <= row0) lo = mid; else hi = mid - 1;
+                if (l.padded[mid] <= row0) lo = mid; else hi = mid - 1;
             }
             e = lo;
         }
         p.tiles[tile] = e;
-        const int valid_end = e >= 0 ? padded[e] + total[e] : 0;
+        const int valid_end = e >= 0 ? l.padded[e] + l.total[e] : 0;
         for (int row = max(row0, valid_end); row < row0 + p.M; ++row) p.slots[row] = A;
     }
+}
+
+// One workgroup builds the whole plan.  With `Fused`, the same workgroup
+// first routes every token (decode-sized batches).
+template <bool Fused, int EP>
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_single_kernel(DispatchArgs p) {
+    extern __shared__ int lds[];
+    const DispatchLds l = dispatch_lds(lds, p.E);
+    const int wave = threadIdx.x >> 6;
+    if constexpr (Fused) {
+        for (int t = wave; t < p.tokens; t += kDispatchWaves) {
+            if (p.logits_bf16)
+                route_token<EP, uint16_t>(p.logits_bf16 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
+            else
+                route_token<EP, float>(p.logits_f32 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    const int A = p.tokens * p.K;
+    span_counts(p, l, 0, A);
+    const int status = l.flag[0];
+    padded_scan(p, l);
+    span_scatter(p, l, 0, A, l.padded);
+    finalize_plan(p, l, status);
+}
+
+// Multi-workgroup plan, step 1: per-chunk expert counts and status.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_hist_kernel(DispatchArgs p) {
+    extern __shared__ int lds[];
+    const DispatchLds l = dispatch_lds(lds, p.E);
+    const int A = p.tokens * p.K, c = blockIdx.x;
+    const int b = c * p.chunk, e_ = min(A, b + p.chunk);
+    span_counts(p, l, b, e_);
+    for (int e = threadIdx.x; e < p.E; e += kDispatchThreads) p.scratch[(size_t)c * p.E + e] = l.total[e];
+    if (threadIdx.x == 0) p.scratch[(size_t)gridDim.x * p.E + c] = l.flag[0];
+}
+
+// Step 2 (one workgroup): chunk bases per expert, padded offsets, metadata.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(DispatchArgs p, int chunks) {
+    extern __shared__ int lds[];
+    const DispatchLds l = dispatch_lds(lds, p.E);
+    int* cnt = l.scan_tmp + kDispatchThreads;  // [chunks][E]
+    const int n = chunks * p.E;
+    for (int i = threadIdx.x; i < n; i += kDispatchThreads) cnt[i] = p.scratch[i];
+    __shared__ int status_word;
+    if (threadIdx.x == 0) status_word = 0;
+    __syncthreads();
+    for (int c = threadIdx.x; c < chunks; c += kDispatchThreads)
+        if (p.scratch[(size_t)chunks * p.E + c]) atomicOr(&status_word, 1);
+    for (int e = threadIdx.x; e < p.E; e += kDispatchThreads) {
+        int run = 0;
+        for (int c = 0; c < chunks; ++c) {
+            const int v = cnt[c * p.E + e];
+            cnt[c * p.E + e] = run;
+            run += v;
+        }
+        l.total[e] = run;
+    }
+    __syncthreads();
+    padded_scan(p, l);
+    for (int i = threadIdx.x; i < n; i += kDispatchThreads) p.scratch[i] = cnt[i] + l.padded[i % p.E];
+    finalize_plan(p, l, status_word);
+}
+
+// Step 3: stable scatter of each chunk from its absolute bases.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(DispatchArgs p) {
+    extern __shared__ int lds[];
+    const DispatchLds l = dispatch_lds(lds, p.E);
+    const int A = p.tokens * p.K, c = blockIdx.x;
+    const int b = c * p.chunk, e_ = min(A, b + p.chunk);
+    span_counts(p, l, b, e_);
+    span_scatter(p, l, b, e_, p.scratch + (size_t)c * p.E);
 }
 
 // Ordered combine: out[t,h] = bf16(sum_r f32(contrib[t*K + r, h])), ranks in order
@@ -359,24 +482,26 @@ size_t dispatch_lds_bytes(int E) {
 }
 
 template <bool Fused>
-int launch_dispatch_ep(DispatchArgs a, hipStream_t s) {
+int launch_dispatch_single(DispatchArgs a, hipStream_t s) {
     const size_t lds = dispatch_lds_bytes(a.E);
     const int ep = (a.E + 63) / 64;
-    if (ep <= 1) dispatch_kernel<Fused, 1><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 2) dispatch_kernel<Fused, 2><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 4) dispatch_kernel<Fused, 4><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 8) dispatch_kernel<Fused, 8><<<1, kDispatchThreads, lds, s>>>(a);
-    else dispatch_kernel<Fused, 16><<<1, kDispatchThreads, lds, s>>>(a);
+    if (ep <= 1) dispatch_single_kernel<Fused, 1><<<1, kDispatchThreads, lds, s>>>(a);
+    else if (ep <= 2) dispatch_single_kernel<Fused, 2><<<1, kDispatchThreads, lds, s>>>(a);
+    else if (ep <= 4) dispatch_single_kernel<Fused, 4><<<1, kDispatchThreads, lds, s>>>(a);
+    else if (ep <= 8) dispatch_single_kernel<Fused, 8><<<1, kDispatchThreads, lds, s>>>(a);
+    else dispatch_single_kernel<Fused, 16><<<1, kDispatchThreads, lds, s>>>(a);
     return (int)hipGetLastError();
 }
 
 }  // namespace
 
-// Largest expert count the routing/dispatch kernels accept (16 logits per lane;
-// the dispatch LDS footprint is (18 E + 1026) words, 75 KB at E = 1024).
-constexpr int kMaxExperts = 1024;
+// Largest expert count the routing/dispatch kernels accept (8 logits per lane;
+// the dispatch LDS footprint is (18 E + 1026) words, 41 KB at E = 512).
+constexpr int kMaxExperts = 512;
 constexpr int kMaxTopK = 32;
 constexpr int kFusedRouteMaxTokens = 256;
+constexpr int kDispatchChunk = 4096;  // assignments per workgroup in the multi-workgroup plan
+constexpr int kPlanLdsWords = 4096;   // [chunks][E] counts staged by the plan workgroup
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M) {
     if (tokens <= 0 || E <= 0 || K <= 0 || M <= 0) return -1;
@@ -397,7 +522,8 @@ int launch_routing(const void* logits, int logits_dtype, float* routes, int toke
 // Dispatch (and, with logits, routing first when the batch is small enough
 // to route inside the dispatch workgroup).
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,
-                    int* tiles, int tokens, int E, int K, int M, int capacity, hipStream_t s) {
+                    int* tiles, int tokens, int E, int K, int M, int capacity, void* scratch, size_t scratch_bytes,
+                    hipStream_t s) {
     if (!routes || !meta || !offsets || !slots || !tiles || tokens <= 0 || E <= 0 || E > kMaxExperts || K <= 0 ||
         K > E || K > kMaxTopK || M <= 0 || capacity <= 0 || capacity % M)
         return kInvalid;
@@ -417,17 +543,32 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
     int bits = 0;
     while ((1 << bits) < E) ++bits;
     a.expert_bits = bits;
+    const int A = tokens * K;
+    // Chunk so that the plan workgroup can stage all [chunks][E] counts in LDS.
+    const int max_chunks = kPlanLdsWords / E;
+    int chunk = kDispatchChunk;
+    if ((A + chunk - 1) / chunk > max_chunks) chunk = ((A + max_chunks - 1) / max_chunks + 1023) / 1024 * 1024;
+    const int chunks = (A + chunk - 1) / chunk;
+    const bool multi = A > kDispatchChunk && scratch && E <= kPlanLdsWords &&
+                       scratch_bytes >= sizeof(int) * ((size_t)chunks * E + chunks);
     if (logits) {
         if (logits_dtype != 0 && logits_dtype != 1) return kInvalid;
-        if (tokens <= kFusedRouteMaxTokens) {
+        if (tokens <= kFusedRouteMaxTokens && !multi) {
             if (logits_dtype == 1) a.logits_bf16 = (const uint16_t*)logits;
             else a.logits_f32 = (const float*)logits;
-            return launch_dispatch_ep<true>(a, s);
+            return launch_dispatch_single<true>(a, s);
         }
         int code = launch_routing(logits, logits_dtype, routes, tokens, E, K, s);
         if (code) return code;
     }
-    return launch_dispatch_ep<false>(a, s);
+    if (!multi) return launch_dispatch_single<false>(a, s);
+    a.scratch = (int*)scratch;
+    a.chunk = chunk;
+    const size_t lds = dispatch_lds_bytes(E);
+    dispatch_hist_kernel<<<chunks, kDispatchThreads, lds, s>>>(a);
+    dispatch_plan_kernel<<<1, kDispatchThreads, lds + sizeof(int) * (size_t)chunks * E, s>>>(a, chunks);
+    dispatch_scatter_kernel<<<chunks, kDispatchThreads, lds, s>>>(a);
+    return (int)hipGetLastError();
 }
 
 int launch_combine(const void* contributions, void* output, const int* status, int tokens, int H, int K,

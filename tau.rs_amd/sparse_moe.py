@@ -53,8 +53,8 @@ class SparseMoeConfig:
             raise ValueError("sparse MoE shared-expert intermediate size must be non-zero")
         if not self.normalize_selected_weights:
             raise ValueError("the HIP path implements normalised top-k weights only")
-        if self.num_experts > 1024 or self.experts_per_token > 32:
-            raise ValueError("the HIP path supports num_experts <= 1024 and experts_per_token <= 32")
+        if self.num_experts > 512 or self.experts_per_token > 32:
+            raise ValueError("the HIP path supports num_experts <= 512 and experts_per_token <= 32")
 
 
 @dataclasses.dataclass(frozen=True)

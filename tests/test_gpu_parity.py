@@ -95,3 +95,48 @@ def test_layer_matches_oracle(tau, oracle, idx):
         say(f"    rel_l2 vs f32 {e32:.2e}  vs bf16-contract {e16:.2e}")
         assert e32 <= 1e-2
         assert e16 <= 2e-3
+
+
+FULL = ["c3_30b_a3b_prefill", "c4_next_sparse", "c5_235b_prefill"]
+
+
+@pytest.mark.parametrize("name", FULL)
+def test_full_size_routing_and_dispatch(tau, oracle, name):
+    """Full benchmark token counts exercise the multi-workgroup dispatch."""
+    shape = tau.inputs.CONFIGS[name]
+    say(f"[full dispatch] {name} T={shape.tokens}")
+    layer = tau.inputs.make_layer(shape)
+    runner, out = run_layer(tau, layer, shape)
+    tile_rows = runner.tile_rows_for(shape.tokens)
+    v = runner.plan_views(shape.tokens)
+    K = shape.top_k
+    routes = to_np(v["routes"])
+    ids_ref, w_ref = oracle.route(to_np(layer["logits"]), K)
+    np.testing.assert_array_equal(routes[:, :K].astype(np.int64), ids_ref)
+    err = np.abs(routes[:, K:] - w_ref)
+    assert np.all(err <= 1e-7 + 1e-5 * np.abs(w_ref)), float(err.max())
+    cap = runner._ws["capacity"]
+    meta, offsets, slots, tiles = oracle.dispatch(ids_ref, shape.experts, tile_rows, cap)
+    np.testing.assert_array_equal(v["meta"].cpu().numpy(), meta)
+    np.testing.assert_array_equal(v["offsets"].cpu().numpy(), offsets)
+    np.testing.assert_array_equal(v["slots"].cpu().numpy()[:cap], slots)
+    np.testing.assert_array_equal(v["tiles"].cpu().numpy()[: cap // tile_rows], tiles)
+    assert np.all(np.isfinite(to_np(out)))
+
+
+@pytest.mark.parametrize("name", ["c3_30b_a3b_prefill", "c4_next_sparse"])
+def test_full_size_layer_sampled_tokens(tau, oracle, name):
+    """Full-size layer; the oracle recomputes a token sample (tokens are independent)."""
+    shape = tau.inputs.CONFIGS[name]
+    say(f"[full layer] {name} T={shape.tokens}")
+    layer = tau.inputs.make_layer(shape)
+    _, out = run_layer(tau, layer, shape)
+    rng = np.random.default_rng(0)
+    mask = np.zeros(shape.tokens, np.uint8)
+    mask[rng.choice(shape.tokens, 96, replace=False)] = 1
+    ids, w = oracle.route(to_np(layer["logits"]), shape.top_k)
+    ref = oracle.moe(to_np(layer["x"]), ids, w, to_np(layer["gate_up"]), to_np(layer["down"]), token_mask=mask)
+    sel = mask.astype(bool)
+    e = rel_l2(to_np(out)[sel], ref[sel])
+    say(f"    rel_l2 vs f32 (96 tokens) {e:.2e}")
+    assert e <= 1e-2
