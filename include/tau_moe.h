@@ -48,7 +48,7 @@ int tau_launch_moe_routing_fp32(const void* logits, float* routes, int rows, voi
 
 /* Replaces tau_launch_moe_prefill_dispatch (cuda_ffi.rs:33-43; moe_dispatch.cu:88-104).
  * meta [514], offsets [257], slots [capacity], tiles [capacity/tile_rows].
- * tile_rows in {16, 32, 64, 128}; capacity >= tau_moe_prefill_capacity(...).
+ * tile_rows in {16, 32, 64, 128, 256}; capacity >= tau_moe_prefill_capacity(...).
  * The permutation is stable (token-ascending inside each expert). */
 int tau_launch_moe_prefill_dispatch(const float* routes, int* meta, int* offsets, int* slots, int* tiles,
                                     int tokens, int capacity, int tile_rows, void* stream);
@@ -120,7 +120,7 @@ int tau_launch_fused_bf16_moe_decode(const void* input, const void* logits, cons
 int64_t tau_moe_prefill_capacity(int tokens, int experts, int top_k, int tile_rows);
 
 /* Row block chosen by the library for a routing shape: 16 selects the
- * weight-streaming decode kernels, 32/64/128 the LDS-tiled MFMA kernels. */
+ * weight-streaming decode kernels (16, 32), 64/128/256 the LDS-tiled MFMA kernels. */
 int tau_moe_select_tile_rows(int tokens, int experts, int top_k, int hidden, int intermediate);
 
 /* Workspace bytes for tau_launch_moe_prefill_ex, in argument order:
@@ -144,7 +144,7 @@ int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, c
 
 /* Whole routed path for any (E, K): routing, dispatch, gate_up+SiLU·mul,
  * down+weight, combine.  tile_rows from tau_moe_select_tile_rows (or any of
- * 16/32/64/128); receipts (optional) receive 10 words, gate_up then down. */
+ * 16/32/64/128/256); receipts (optional) receive 10 words, gate_up then down. */
 int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_dtype, const void* gate_up,
                               const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                               void* activated, void* contributions, void* output, int tokens, int hidden,

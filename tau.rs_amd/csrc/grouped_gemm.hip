@@ -578,6 +578,325 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS pipelined MFMA kernel (prefill, K a multiple of 64)
+// ---------------------------------------------------------------------------
+// Block tile BM x BN x 64; WM x WN waves, each owning a (BM/WM) x (BN/WN) grid
+// of 32x32x16 MFMAs.  Operand panels move HBM -> LDS with global_load_lds
+// (16 bytes per lane, no VGPR staging) into STAGES ring buffers; rows are 128
+// bytes with the 16-byte chunk index XOR-swizzled by (row & 7), so the
+// fragment reads (32 rows x 16 bytes per half-wave) spread over all banks.
+// One barrier per K step: waiting on the oldest stage's loads, the barrier,
+// then the next loads into the stage every wave has just finished with.
+// The epilogue stages the BF16 tile in LDS and writes 16-byte row segments,
+// scattered by slot for the down projection.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// XOR swizzle of the 16-byte chunk slot within a staged row.  LDS has 64
+// banks of 4 bytes (256 bytes); a 16-lane phase of a fragment read touches 16
+// consecutive rows at one chunk, so (row bank offset, swizzled slot) must be
+// distinct over any 16 consecutive rows: 128-byte rows (BK=64) alternate two
+// bank offsets, so the key is (row >> 1) & 7; 64-byte rows (BK=32) cycle four
+// offsets, so the key is (row >> 2) & 3.
+template <int CPR>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (CPR == 8) return (row >> 1) & 7;
+    else return (row >> 2) & 3;
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int PD = 0>
+__global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int MI = TM / 32, NI = TN / 32;
+    static_assert(MI >= 1 && NI >= 1, "wave tile too small");
+    static_assert(EPI != kEpiSilu || NI % 2 == 0, "SiLU pairs gate/up blocks");
+    static_assert(EPI != kEpiStoreF32, "f32 outputs use lds_gemm");
+    constexpr int CPR = BK / 8;                          // 16-byte chunks per staged row
+    constexpr int RPI = 64 / CPR;                        // rows filled by one wave instruction
+    constexpr int ACH = BM * CPR / NT, BCH = BN * CPR / NT;  // 16-byte chunks per thread per stage
+    static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/threads mismatch");
+    constexpr int L = ACH + BCH;                         // loads per thread per stage
+    constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
+    constexpr int STAGE_ELEMS = (BM + BN) * BK;
+    constexpr int CSTRIDE = NOUT + 8;                    // epilogue tile row stride (elements)
+    constexpr int SMEM_ELEMS = STAGES * STAGE_ELEMS > BM * CSTRIDE ? STAGES * STAGE_ELEMS : BM * CSTRIDE;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM_ELEMS];
+    __shared__ long row_src[BM];   // gather: source row of A; down: destination slot (or -1)
+    __shared__ float row_w[BM];    // down: route weight
+    __shared__ uint32_t junk[WM * WN * 64];  // landing area of the L2 prefetches
+    static_assert(PD == 0 || STAGES == 2, "L2 prefetch is scheduled for two stages");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    if (p.receipt && blockIdx.x == 0 && tid == 0) {
+        p.receipt[0] = BM; p.receipt[1] = BN; p.receipt[2] = BK; p.receipt[3] = WM * WN; p.receipt[4] = STAGES;
+    }
+    const int n_tiles = (p.n + NOUT - 1) / NOUT;
+    const int live = live_blocks(p, BM);
+    const int total = live * n_tiles;
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    const int item = xcd_remap(blockIdx.x, per_xcd);
+    if (item < 0 || item >= total) return;
+    const int m_tile = item / n_tiles, n_tile = item - m_tile * n_tiles;
+    const int expert = p.tiles ? p.tiles[m_tile] : 0;
+    const int row0 = m_tile * BM;
+    const int c0 = n_tile * NOUT;
+    if (expert < 0) {
+        if constexpr (EPI == kEpiStoreBf16) {  // dead capacity reads as zeros
+            uint16_t* out = (uint16_t*)p.out;
+            for (int i = tid; i < BM * NOUT; i += NT) {
+                const int r = row0 + i / NOUT, c = c0 + i % NOUT;
+                if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
+            }
+        }
+        return;
+    }
+
+    // Row table: A source rows (gather), destination slots and weights (down).
+    for (int r = tid; r < BM; r += NT) {
+        const int row = row0 + r;
+        long src = -1;
+        float w = 0.f;
+        if (row < p.rows) {
+            if constexpr (AM == kAGather || EPI == kEpiScatterWeighted) {
+                const int slot = p.slots[row];
+                if (slot >= 0 && slot < p.assignments) {
+                    if constexpr (AM == kAGather) src = slot / p.topk;
+                    else src = slot;
+                    if constexpr (EPI == kEpiScatterWeighted) {
+                        const int t = slot / p.topk, rk = slot - t * p.topk;
+                        w = p.routes[(size_t)t * 2 * p.topk + p.topk + rk];
+                    }
+                }
+            } else {
+                src = row;
+            }
+        }
+        row_src[r] = src;
+        row_w[r] = w;
+    }
+    __syncthreads();
+
+    // Per-lane load sources.  Instruction i of wave w fills rows
+    // [q*RPI, (q+1)*RPI) with q = i*(NT/64) + w; lane l supplies row
+    // q*RPI + l/CPR into chunk slot l%CPR, i.e. global chunk slot ^ swz(row).
+    const int lrow8 = lane / CPR;
+    const uint16_t* a_src[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+        const int r = (i * (NT / 64) + wave) * RPI + lrow8;
+        const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
+        long src_row;
+        if constexpr (AM == kAGather) {
+            const long s_ = row_src[r];
+            src_row = s_ >= 0 ? s_ : 0;  // padding rows read row 0; their outputs are dropped
+        } else {
+            src_row = row0 + r < p.rows ? row0 + r : 0;
+        }
+        a_src[i] = p.a + src_row * (long)p.lda + kchunk;
+    }
+    const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
+    const uint16_t* b_src[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+        const int r = (i * (NT / 64) + wave) * RPI + lrow8;
+        const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
+        long wrow;
+        if constexpr (EPI == kEpiSilu) {
+            const int j = c0 + (r < BN / 2 ? r : r - BN / 2);
+            wrow = j < p.n ? (r < BN / 2 ? j : j + p.w_up_offset) : 0;
+        } else {
+            const int j = c0 + r;
+            wrow = j < p.n ? j : 0;
+        }
+        b_src[i] = wexp + wrow * (long)p.k + kchunk;
+    }
+
+    // L2 prefetch: thread t < BM + BN touches one 128-byte line of staged row t
+    // PD K-tiles ahead (4-byte global_load_lds into `junk`), so HBM sees more
+    // bytes in flight than the LDS stages alone can hold.
+    constexpr int PF_ROWS = BM + BN;
+    constexpr int PF_WAVES = (PF_ROWS + 63) / 64;  // waves that issue a prefetch
+    const uint16_t* pf_src = nullptr;
+    if constexpr (PD > 0) {
+        const int r = tid < PF_ROWS ? tid : 0;
+        if (r < BM) {
+            long src_row;
+            if constexpr (AM == kAGather) src_row = row_src[r] >= 0 ? row_src[r] : 0;
+            else src_row = row0 + r < p.rows ? row0 + r : 0;
+            pf_src = p.a + src_row * (long)p.lda;
+        } else {
+            const int rb = r - BM;
+            long wrow;
+            if constexpr (EPI == kEpiSilu) {
+                const int j = c0 + (rb < BN / 2 ? rb : rb - BN / 2);
+                wrow = j < p.n ? (rb < BN / 2 ? j : j + p.w_up_offset) : 0;
+            } else {
+                const int j = c0 + rb;
+                wrow = j < p.n ? j : 0;
+            }
+            pf_src = wexp + wrow * (long)p.k;
+        }
+    }
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    auto prefetch = [&](int kt) {
+        if (wave < PF_WAVES)
+            __builtin_amdgcn_global_load_lds((const void*)(pf_src + kt * BK), (lds_ptr)(junk + wave * 64), 4, 0, 0);
+    };
+    auto issue = [&](int kt, int stage) {
+        uint16_t* As = smem + stage * STAGE_ELEMS;
+        uint16_t* Bs = As + BM * BK;
+        const int kb = kt * BK;
+#pragma unroll
+        for (int i = 0; i < ACH; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + kb),
+                                             (lds_ptr)(As + (i * (NT / 64) + wave) * 512), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BCH; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(b_src[i] + kb),
+                                             (lds_ptr)(Bs + (i * (NT / 64) + wave) * 512), 16, 0, 0);
+    };
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+
+    const int nk = p.k / BK;
+#pragma unroll
+    for (int s_ = 0; s_ < STAGES - 1; ++s_)
+        if (s_ < nk) issue(s_, s_);
+    if constexpr (PD > 0)
+        for (int d = 1; d < PD && d < nk; ++d) prefetch(d);
+
+    const int lr = lane & 31, lh = lane >> 5;
+    // Fragment reads of one 16-deep K step; the next step's reads are issued
+    // before the current step's MFMAs so LDS latency hides under the MFMAs.
+    auto frags = [&](const uint16_t* As, const uint16_t* Bs, int ks, bf16x8* af, bf16x8* bfr) {
+        const int c = ks * 2 + lh;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const int r = wm * TM + i * 32 + lr;
+            af[i] = as_bf16x8(*(const u32x4*)(As + r * BK + ((c ^ swz<CPR>(r)) * 8)));
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            int r;
+            if constexpr (EPI == kEpiSilu) {
+                const int jj = j < NI / 2 ? j : j - NI / 2;
+                r = (j < NI / 2 ? 0 : BN / 2) + wn * (TN / 2) + jj * 32 + lr;
+            } else {
+                r = wn * TN + j * 32 + lr;
+            }
+            bfr[j] = as_bf16x8(*(const u32x4*)(Bs + r * BK + ((c ^ swz<CPR>(r)) * 8)));
+        }
+    };
+    for (int kt = 0; kt < nk; ++kt) {
+        // Tile kt's loads are done once at most the later-issued loads remain
+        // (VMEM loads complete in order).
+        if constexpr (PD > 0) {
+            // Issued after tile kt's stage: the prefetch(es) of the previous
+            // iteration (or of the prologue for kt == 0), by prefetching waves.
+            if (wave < PF_WAVES && kt > 0 && kt - 1 + PD < nk) wait_vmcnt<1>();
+            else if (wave < PF_WAVES && kt == 0 && PD == 2 && nk > 1) wait_vmcnt<1>();
+            else wait_vmcnt<0>();
+        } else {
+            if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
+            else wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        if constexpr (PD > 0)
+            if (kt + PD < nk) prefetch(kt + PD);
+        const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
+        const uint16_t* Bs = As + BM * BK;
+        bf16x8 af[2][MI], bfr[2][NI];
+        frags(As, Bs, 0, af[0], bfr[0]);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            if (ks + 1 < BK / 16) frags(As, Bs, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // stages are reused for the output tile
+
+    // Epilogue 1: accumulators -> BF16 tile in LDS.  Value q of lane l sits at
+    // row (q/4)*8 + (l/32)*4 + q%4, column l%32 of its 32x32 block.
+    uint16_t* C = smem;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int r = wm * TM + i * 32 + (q >> 2) * 8 + lh * 4 + (q & 3);
+            if constexpr (EPI == kEpiSilu) {
+#pragma unroll
+                for (int j = 0; j < NI / 2; ++j) {
+                    const float g = round_bf16(acc[i][j][q]);
+                    const float u = round_bf16(acc[i][j + NI / 2][q]);
+                    C[r * CSTRIDE + wn * (TN / 2) + j * 32 + lr] = float_to_bf16_bits(silu(g) * u);
+                }
+            } else {
+                const float w = EPI == kEpiScatterWeighted ? row_w[r] : 1.0f;
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const float v = EPI == kEpiScatterWeighted ? acc[i][j][q] * w : acc[i][j][q];
+                    C[r * CSTRIDE + wn * TN + j * 32 + lr] = float_to_bf16_bits(v);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // Epilogue 2: 16-byte row segments to global memory.
+    constexpr int SEGS = NOUT / 8;
+    uint16_t* out = (uint16_t*)p.out;
+    const bool vec = (p.ldo % 8) == 0 && ((uintptr_t)p.out % 16) == 0;
+    for (int i = tid; i < BM * SEGS; i += NT) {
+        const int r = i / SEGS, sg = i - r * SEGS;
+        const int row = row0 + r;
+        if (row >= p.rows) continue;
+        long dst;
+        if constexpr (EPI == kEpiScatterWeighted) {
+            dst = row_src[r];
+            if (dst < 0) continue;
+        } else {
+            dst = row;
+        }
+        const int col = c0 + sg * 8;
+        if (col >= p.n) continue;
+        const uint16_t* src = C + r * CSTRIDE + sg * 8;
+        uint16_t* o = out + dst * (long)p.ldo + col;
+        if (vec && col + 8 <= p.n) {
+            *(u32x4*)o = *(const u32x4*)src;
+        } else {
+            for (int e = 0; e < 8 && col + e < p.n; ++e) o[e] = src[e];
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int PD = 0>
+int launch_mfma(const GemmArgs& p, hipStream_t s) {
+    constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
+    const long m_blocks = (p.rows + BM - 1) / BM;
+    const long n_tiles = (p.n + NOUT - 1) / NOUT;
+    const long grid = (m_blocks * n_tiles + kXcds - 1) / kXcds * kXcds;
+    if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
+    mfma_gemm<BM, BN, WM, WN, STAGES, AM, EPI, BK, PD><<<(unsigned)grid, 64 * WM * WN, 0, s>>>(p);
+    return (int)hipGetLastError();
+}
+
 template <int BM, int BN, int WM, int WN, int AM, int EPI>
 int launch_lds(const GemmArgs& p, bool aligned, hipStream_t s) {
     constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
@@ -616,13 +935,32 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
+// Row block -> kernel.  Every kernel's row block must equal `bm`: dispatch
+// built tiles[] (one expert per bm rows) and the kernels index it per block.
+// 16/32: weight streaming; 64/128/256: direct-to-LDS
+// MFMA tiles (64x256 with 4 waves, 128x128 with 4 waves, 256x256 with 16
+// waves), measured best on MI355X for the prefill shapes; shapes the MFMA
+// kernel cannot take (K not a multiple of 64, unaligned rows, FP32 output)
+// use the register-staged LDS kernel.
 template <int AM, int EPI>
 int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
+    const bool mfma_ok = aligned && p.k % 64 == 0 && EPI != kEpiStoreF32;
+    if constexpr (EPI != kEpiStoreF32) {
+        if (mfma_ok) {
+            switch (bm) {
+                case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI>(p, s);
+                case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI>(p, s);
+                case 256: return launch_mfma<256, 256, 8, 2, 2, AM, EPI>(p, s);
+                default: break;
+            }
+        }
+    }
     switch (bm) {
         case 16: return launch_stream<AM, EPI, 1>(p, aligned, s);
         case 32: return aligned ? launch_stream<AM, EPI, 2>(p, aligned, s) : launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
         case 64: return launch_lds<64, 128, 2, 2, AM, EPI>(p, aligned, s);
         case 128: return launch_lds<128, 128, 2, 2, AM, EPI>(p, aligned, s);
+        case 256: return launch_lds<256, 128, 4, 2, AM, EPI>(p, aligned, s);
         default: return kInvalid;
     }
 }
@@ -630,8 +968,9 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
 }  // namespace
 
 // Row-block sizes of the compiled kernels: 16 (weight streaming) and
-// 32/64/128 (LDS-tiled MFMA).  Dispatch must pad experts to the same M.
-bool gemm_rows_supported(int bm) { return bm == 16 || bm == 32 || bm == 64 || bm == 128; }
+// 32 (streaming, two row groups) and 64/128/256 (LDS-tiled MFMA).  Dispatch must
+// pad experts to the same M.
+bool gemm_rows_supported(int bm) { return bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == 256; }
 
 int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s) {
     if (!p.a || !p.w || !p.out || p.rows <= 0 || p.n <= 0 || p.k <= 0 || p.lda < p.k || p.ldo < p.n)

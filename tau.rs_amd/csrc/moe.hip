@@ -29,7 +29,7 @@ inline hipStream_t as_stream(void* s) { return (hipStream_t)s; }
 // The reference catalog of prefill tiles (crates/cuda-kernels/src/moe/config.rs:38-76).
 bool reference_tile_ok(const TauGemmTile* c) {
     if (!c) return false;
-    const bool m = c->m == 16 || c->m == 32 || c->m == 64 || c->m == 128;
+    const bool m = c->m == 16 || c->m == 32 || c->m == 64 || c->m == 128 || c->m == 256;
     const bool n = c->n == 16 || c->n == 32 || c->n == 64 || c->n == 128;
     const bool k = c->k == 16 || c->k == 32 || c->k == 64 || c->k == 128;
     const bool w = c->warps == 1 || c->warps == 2 || c->warps == 4 || c->warps == 8;
@@ -111,7 +111,8 @@ int tau_moe_select_tile_rows(int tokens, int experts, int top_k, int hidden, int
     const double rows_per_expert = (double)tokens * top_k / experts;
     if (rows_per_expert <= 16.0) return 16;
     if (rows_per_expert <= 96.0) return 64;
-    return 128;
+    if (rows_per_expert <= 384.0) return 128;
+    return 256;
 }
 
 int tau_moe_workspace_bytes(int tokens, int hidden, int intermediate, int experts, int top_k, int tile_rows,

@@ -9,80 +9,83 @@
 // native layout (crates/cuda-kernels/src/kernels/moe_routing.cu:15-52,
 // moe_dispatch.cuh:9, moe_dispatch.cu:11-85), generalised from E=256/K=8.
 //
-// CDNA4 design: one 64-lane wavefront per token; each lane owns E/64 logits,
-// ordering decisions use 64-bit (score, ~id) keys reduced with DPP/ds_swizzle
-// shuffles, so a top-K costs K wave reductions and no shared memory.  Dispatch
-// is one 1024-thread workgroup: 16 waves each own a contiguous assignment
-// segment, count it, prefix the per-wave counts per expert, and scatter with
-// ballot-derived in-wave ranks, so the permutation is deterministic and
-// token-ascending without atomics on global memory.
+// CDNA4 design.
+//  * Routing: one 16-lane DPP row per token, four tokens per wavefront.  Each
+//    lane owns E/16 logits; max, sum and the K arg-max steps are row-local DPP
+//    butterflies (quad_perm, row_half_mirror, row_mirror), so a top-K costs no
+//    LDS or cross-lane memory traffic and the four tokens of a wave proceed
+//    together.  Ordering keys are (x - max, ~id) in 64 bits: exp is monotone,
+//    so they order experts exactly as the probabilities do, ties included,
+//    whatever the rounding of exp.
+//  * Dispatch: a counting sort.  Every assignment's expert is staged in LDS,
+//    16 waves each count a contiguous segment (ballot-derived peer masks, no
+//    global atomics), counts are prefixed per expert over waves and over
+//    workgroup chunks, and each assignment lands at
+//    offset[e] + earlier-chunk count + earlier-wave count + in-wave rank, which
+//    is the token-ascending order of the reference's CPU plan.  Small batches
+//    run route + plan + scatter in one workgroup; large ones use three
+//    launches (route+histogram per chunk, plan, scatter per chunk).
 #include "kernels.hpp"
 
 namespace tau_amd {
 namespace {
 
+// ---------------------------------------------------------------------------
+// Row (16-lane) DPP reductions; every lane of the row receives the result.
+// ---------------------------------------------------------------------------
+constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kRowHalfMirror = 0x141, kRowMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, 0xf, 0xf, false);
+}
+template <int Ctrl>
+__device__ __forceinline__ float dppf(float v) {
+    return __uint_as_float(dpp<Ctrl>(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dppf<kQuadXor1>(v));
+    v = fmaxf(v, dppf<kQuadXor2>(v));
+    v = fmaxf(v, dppf<kRowHalfMirror>(v));
+    v = fmaxf(v, dppf<kRowMirror>(v));
+    return v;
+}
+
+__device__ __forceinline__ float row_sum(float v) {
+    v += dppf<kQuadXor1>(v);
+    v += dppf<kQuadXor2>(v);
+    v += dppf<kRowHalfMirror>(v);
+    v += dppf<kRowMirror>(v);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t row_or(uint32_t v) {
+    v |= dpp<kQuadXor1>(v);
+    v |= dpp<kQuadXor2>(v);
+    v |= dpp<kRowHalfMirror>(v);
+    v |= dpp<kRowMirror>(v);
+    return v;
+}
+
+template <int Ctrl>
+__device__ __forceinline__ uint64_t max_step(uint64_t v) {
+    const uint64_t o = ((uint64_t)dpp<Ctrl>((uint32_t)(v >> 32)) << 32) | dpp<Ctrl>((uint32_t)v);
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t row_max_u64(uint64_t v) {
+    v = max_step<kQuadXor1>(v);
+    v = max_step<kQuadXor2>(v);
+    v = max_step<kRowHalfMirror>(v);
+    v = max_step<kRowMirror>(v);
+    return v;
+}
+
 // Order-preserving map of an FP32 value onto uint32 (larger float -> larger key).
 __device__ __forceinline__ uint32_t orderable(float v) {
     uint32_t u = __float_as_uint(v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Wave-wide reductions built from DPP lane moves (no LDS traffic): butterfly
-// inside each 16-lane row, then row_bcast:15 / row_bcast:31 carry the row
-// results upward so lane 63 holds the full reduction, read back uniformly.
-template <int Ctrl, int RowMask>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t identity, uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, Ctrl, RowMask, 0xf, false);
-}
-
-template <int Ctrl, int RowMask>
-__device__ __forceinline__ float dpp_f32(float identity, float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), Ctrl, RowMask,
-                                                      0xf, false));
-}
-
-constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kRowHalfMirror = 0x141, kRowMirror = 0x140;
-constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
-
-__device__ __forceinline__ float wave_max_f32(float v) {
-    const float id = -INFINITY;
-    v = fmaxf(v, dpp_f32<kQuadXor1, 0xf>(id, v));
-    v = fmaxf(v, dpp_f32<kQuadXor2, 0xf>(id, v));
-    v = fmaxf(v, dpp_f32<kRowHalfMirror, 0xf>(id, v));
-    v = fmaxf(v, dpp_f32<kRowMirror, 0xf>(id, v));
-    v = fmaxf(v, dpp_f32<kRowBcast15, 0xa>(id, v));
-    v = fmaxf(v, dpp_f32<kRowBcast31, 0xc>(id, v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-__device__ __forceinline__ float wave_sum_f32(float v) {
-    v += dpp_f32<kQuadXor1, 0xf>(0.f, v);
-    v += dpp_f32<kQuadXor2, 0xf>(0.f, v);
-    v += dpp_f32<kRowHalfMirror, 0xf>(0.f, v);
-    v += dpp_f32<kRowMirror, 0xf>(0.f, v);
-    v += dpp_f32<kRowBcast15, 0xa>(0.f, v);
-    v += dpp_f32<kRowBcast31, 0xc>(0.f, v);
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-template <int Ctrl, int RowMask>
-__device__ __forceinline__ uint64_t max_step_u64(uint64_t v) {
-    const uint32_t lo = dpp_u32<Ctrl, RowMask>(0u, (uint32_t)v);
-    const uint32_t hi = dpp_u32<Ctrl, RowMask>(0u, (uint32_t)(v >> 32));
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    return o > v ? o : v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    v = max_step_u64<kQuadXor1, 0xf>(v);
-    v = max_step_u64<kQuadXor2, 0xf>(v);
-    v = max_step_u64<kRowHalfMirror, 0xf>(v);
-    v = max_step_u64<kRowMirror, 0xf>(v);
-    v = max_step_u64<kRowBcast15, 0xa>(v);
-    v = max_step_u64<kRowBcast31, 0xc>(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
 }
 
 template <typename T>
@@ -94,103 +97,110 @@ __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p, size_t 
     return bf16_bits_to_float(p[i]);
 }
 
-// Routes one token with the calling wave.  `row` points at the token's logits,
-// `out` at its packed [2K] routes row.
+// Routes token `t` with the calling 16-lane row.  Writes the packed routes row
+// and, when `eids` is non-null, the K selected experts (or -1 for every rank
+// of a rejected row) at eids[0..K).  Returns true when the row was rejected.
+// Rows with `active == false` take part in the DPP steps but write nothing.
 template <int EP, typename T>
-__device__ __forceinline__ void route_token(const T* row, float* out, int E, int K) {
-    const int lane = threadIdx.x & 63;
-    float d[EP], p[EP];
-    bool finite = true;
+__device__ __forceinline__ bool route_row(const T* logits, int t, bool active, float* routes, int E, int K,
+                                          int* eids) {
+    const int l16 = threadIdx.x & 15;
+    const T* row = logits + (size_t)(active ? t : 0) * E;
+    float d[EP], p[EP];  // p: exp(x - max) numerators
+    uint32_t nonfinite = 0;
     float maximum = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EP; ++j) {
-        int e = j * 64 + lane;
+        const int e = j * 16 + l16;
         d[j] = e < E ? load_logit<T>(row, e) : -INFINITY;
-        if (e < E) finite &= __builtin_isfinite(d[j]);
+        if (e < E && !__builtin_isfinite(d[j])) nonfinite = 1;
         maximum = fmaxf(maximum, d[j]);
     }
-    if (!__all(finite)) {
-        for (int i = lane; i < 2 * K; i += 64) out[i] = __builtin_nanf("");
-        return;
-    }
-    maximum = wave_max_f32(maximum);
+    nonfinite = row_or(nonfinite);
+    maximum = row_max(maximum);
     float local = 0.f;
 #pragma unroll
     for (int j = 0; j < EP; ++j) {
-        int e = j * 64 + lane;
-        // x - max, with -0 folded onto +0 so equal probabilities give equal keys.
-        d[j] = (d[j] - maximum) + 0.0f;
-        p[j] = e < E ? expf(d[j]) : 0.f;
+        const int e = j * 16 + l16;
+        d[j] = (d[j] - maximum) + 0.0f;  // -0 folded onto +0: equal values, equal keys
+        p[j] = e < E ? expf(d[j]) : 0.f;  // numerators; divided only once selected
         local += p[j];
     }
-    const float denominator = wave_sum_f32(local);
-#pragma unroll
-    for (int j = 0; j < EP; ++j) p[j] = p[j] / denominator;
+    const float denominator = row_sum(local);
 
-    // exp is monotone, so (x - max) orders experts exactly as their
-    // probabilities do, ties included, without depending on exp rounding.
     uint32_t taken = 0;
     float selected_sum = 0.f;
-    float my_weight = 0.f;
-    int my_id = 0;
+    int my_id[2] = {0, 0};
+    float my_p[2] = {0.f, 0.f};
     for (int r = 0; r < K; ++r) {
         uint64_t best = 0;
 #pragma unroll
         for (int j = 0; j < EP; ++j) {
-            int e = j * 64 + lane;
+            const int e = j * 16 + l16;
             if (e < E && !(taken & (1u << j))) {
-                uint64_t key = ((uint64_t)orderable(d[j]) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+                const uint64_t key = ((uint64_t)orderable(d[j]) << 32) | (0xffffffffu - (uint32_t)e);
                 best = key > best ? key : best;
             }
         }
-        best = wave_max_u64(best);
-        const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-        const int owner = id & 63, slot = id >> 6;
+        best = row_max_u64(best);
+        const int id = (int)(0xffffffffu - (uint32_t)best);
+        const int owner = id & 15, slot = id >> 4;
         float mine = 0.f;
 #pragma unroll
         for (int j = 0; j < EP; ++j)
-            if (j == slot) mine = p[j];
-        const float prob = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), owner));
-        if (lane == owner) taken |= 1u << slot;
+            if (j == slot && l16 == owner) mine = p[j];
+        // Softmax probability of the selected expert, exp(x - max) / sum.
+        const float prob = row_sum(mine) / denominator;  // one non-zero term: exact sum
+        if (l16 == owner) taken |= 1u << slot;
         selected_sum += prob;  // rank order, as routing.rs:187-191
-        if (lane == r) { my_id = id; my_weight = prob; }
+        if (l16 == (r & 15)) {
+            my_id[r >> 4] = id;
+            my_p[r >> 4] = prob;
+        }
     }
-    if (lane < K) {
-        out[lane] = (float)my_id;
-        out[K + lane] = my_weight / selected_sum;
+    if (active) {
+        float* out = routes + (size_t)t * 2 * K;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int rank = s * 16 + l16;
+            if (rank < K) {
+                out[rank] = nonfinite ? __builtin_nanf("") : (float)my_id[s];
+                out[K + rank] = nonfinite ? __builtin_nanf("") : my_p[s] / selected_sum;
+                if (eids) eids[rank] = nonfinite ? -1 : my_id[s];
+            }
+        }
     }
+    return nonfinite != 0;
 }
 
 template <int EP, typename T>
 __global__ __launch_bounds__(256) void route_kernel(const T* logits, float* routes, int T_, int E, int K) {
-    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (token >= T_) return;
-    route_token<EP, T>(logits + (size_t)token * E, routes + (size_t)token * 2 * K, E, K);
+    const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
+    route_row<EP, T>(logits, t, t < T_, routes, E, K, nullptr);
 }
 
-// --------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
 // Dispatch
-// --------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kSpanLds = 4096;      // assignments whose experts fit the LDS stage
+constexpr int kPlanLdsWords = 4096; // [chunks][E] counts staged by the plan workgroup
 
-constexpr int kDispatchThreads = 1024;
-constexpr int kDispatchWaves = kDispatchThreads / 64;
-
-// Reads and validates one assignment (moe_dispatch.cu:23-33 of the reference):
-// a finite integral id in [0,E), no duplicate among the token's earlier ranks,
-// and a finite non-negative weight.  Returns the expert or -1.
+// Validates one externally supplied assignment (moe_dispatch.cu:23-33 of the
+// reference): a finite integral id in [0,E), no duplicate among the token's
+// earlier ranks, a finite non-negative weight.  Returns the expert or -1.
 __device__ __forceinline__ int assignment_expert(const float* routes, int a, int K, int E) {
     const int t = a / K, r = a - t * K;
     const float* row = routes + (size_t)t * 2 * K;
     const float id = row[r], w = row[K + r];
     bool valid = __builtin_isfinite(id) && id >= 0.f && id < (float)E && floorf(id) == id &&
                  __builtin_isfinite(w) && w >= 0.f;
-    // No short-circuit: the earlier-rank loads are independent and issue together.
-    for (int q = 0; q < r; ++q) valid &= row[q] != id;
+    for (int q = 0; q < r; ++q) valid &= row[q] != id;  // independent loads, issued together
     return valid ? (int)id : -1;
 }
 
-// In-wave stable rank of this lane among active lanes holding the same expert.
-// Returns the peer mask (lanes with the same expert).
+// Lanes of the wave holding the same expert (ballot over the id bits).
 __device__ __forceinline__ uint64_t match_expert(int e, bool active, int bits) {
     uint64_t peers = __ballot(active);
     for (int b = 0; b < bits; ++b) {
@@ -202,18 +212,18 @@ __device__ __forceinline__ uint64_t match_expert(int e, bool active, int bits) {
 }
 
 struct DispatchArgs {
-    const uint16_t* logits_bf16;  // fused routing (small T) or null
-    const float* logits_f32;
+    const void* logits;  // routing input (null: routes given)
+    int logits_bf16;
     float* routes;
     int* meta;
     int* offsets;
     int* slots;
     int* tiles;
-    int* scratch;  // multi-workgroup: [chunks][E] counts, then bases; [chunks] flags
+    int* scratch;  // multi-workgroup: [chunks][E] counts -> bases; [chunks] flags
     int tokens, E, K, M;
     int capacity;
     int expert_bits;
-    int chunk;     // assignments per workgroup chunk (multiple of 1024)
+    int chunk_tokens;  // tokens per workgroup chunk (multi-workgroup plan)
 };
 
 struct DispatchLds {
@@ -221,48 +231,69 @@ struct DispatchLds {
     int* total;     // [E] counts of this workgroup's span
     int* padded;    // [E + 1] padded exclusive scan
     int* flag;      // [1]
-    int* scan_tmp;  // [kDispatchThreads]
+    int* scan_tmp;  // [kThreads]
+    int* eids;      // [kSpanLds] expert of each assignment of the span
 };
+
+__host__ __device__ inline size_t dispatch_lds_words(int E) {
+    return (size_t)kWaves * E + E + E + 1 + 1 + kThreads + kSpanLds;
+}
 
 __device__ __forceinline__ DispatchLds dispatch_lds(int* lds, int E) {
     DispatchLds l;
     l.wcount = lds;
-    l.total = lds + kDispatchWaves * E;
+    l.total = lds + kWaves * E;
     l.padded = l.total + E;
     l.flag = l.padded + E + 1;
     l.scan_tmp = l.flag + 1;
+    l.eids = l.scan_tmp + kThreads;
     return l;
 }
 
-// Per-wave counts of [span_begin, span_end), each wave a contiguous segment;
-// then per-expert exclusive prefix over waves (wcount becomes per-wave bases)
-// and total[e] = count of e in the span.  Sets flag on any invalid route.
-__device__ void span_counts(const DispatchArgs& p, const DispatchLds& l, int span_begin, int span_end) {
+// Expert of assignment a of the span: from the LDS stage when it holds the span.
+struct SpanExperts {
+    const int* lds;  // null: read and validate routes in global memory
+    int begin;
+    __device__ __forceinline__ int get(const DispatchArgs& p, int a) const {
+        return lds ? lds[a - begin] : assignment_expert(p.routes, a, p.K, p.E);
+    }
+};
+
+// Stages the span's validated experts in LDS (span <= kSpanLds); sets flag on
+// any invalid assignment.
+__device__ void stage_span(const DispatchArgs& p, const DispatchLds& l, int begin, int end) {
+    bool bad = false;
+    for (int a = begin + (int)threadIdx.x; a < end; a += kThreads) {
+        const int e = assignment_expert(p.routes, a, p.K, p.E);
+        l.eids[a - begin] = e;
+        bad |= e < 0;
+    }
+    if (bad) l.flag[0] = 1;
+}
+
+// Per-wave counts of [begin, end) (each wave a contiguous segment), then the
+// per-expert exclusive prefix over waves; total[e] = count of e in the span.
+__device__ void span_counts(const DispatchArgs& p, const DispatchLds& l, int begin_, int end_, SpanExperts src,
+                            bool check) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < kDispatchWaves * p.E; i += kDispatchThreads) l.wcount[i] = 0;
-    if (tid == 0) l.flag[0] = 0;
-    __syncthreads();
-    const int n = span_end - span_begin;
-    const int seg = ((n + kDispatchWaves - 1) / kDispatchWaves + 63) / 64 * 64;
-    const int begin = span_begin + wave * seg, end = min(span_end, begin + seg);
+    const int n = end_ - begin_;
+    const int seg = ((n + kWaves - 1) / kWaves + 63) / 64 * 64;
+    const int begin = begin_ + wave * seg, end = min(end_, begin + seg);
     int* my = l.wcount + wave * p.E;
     bool bad = false;
     for (int a0 = begin; a0 < end; a0 += 64) {
         const int a = a0 + lane;
-        int e = -1;
-        if (a < end) {
-            e = assignment_expert(p.routes, a, p.K, p.E);
-            bad |= e < 0;
-        }
+        const int e = a < end ? src.get(p, a) : -1;
+        if (check && a < end) bad |= e < 0;
         const bool active = e >= 0;
         const uint64_t peers = match_expert(e, active, p.expert_bits);
         if (active && (peers & lanemask_lt()) == 0) my[e] += __popcll(peers);
     }
-    if (__any(bad) && lane == 0) l.flag[0] = 1;
+    if (check && __any(bad) && lane == 0) l.flag[0] = 1;
     __syncthreads();
-    for (int e = tid; e < p.E; e += kDispatchThreads) {
+    for (int e = tid; e < p.E; e += kThreads) {
         int run = 0;
-        for (int w = 0; w < kDispatchWaves; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
             const int c = l.wcount[w * p.E + e];
             l.wcount[w * p.E + e] = run;
             run += c;
@@ -272,18 +303,17 @@ __device__ void span_counts(const DispatchArgs& p, const DispatchLds& l, int spa
     __syncthreads();
 }
 
-// Stable scatter of the span: slot position = base[e] + per-wave base + in-wave rank.
-__device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int span_begin, int span_end,
-                             const int* base /* [E], LDS or global */) {
+// Stable scatter of the span: slot = base[e] + per-wave base + in-wave rank.
+__device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int begin_, int end_, SpanExperts src,
+                             const int* base) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n = span_end - span_begin;
-    const int seg = ((n + kDispatchWaves - 1) / kDispatchWaves + 63) / 64 * 64;
-    const int begin = span_begin + wave * seg, end = min(span_end, begin + seg);
+    const int n = end_ - begin_;
+    const int seg = ((n + kWaves - 1) / kWaves + 63) / 64 * 64;
+    const int begin = begin_ + wave * seg, end = min(end_, begin + seg);
     int* my = l.wcount + wave * p.E;
     for (int a0 = begin; a0 < end; a0 += 64) {
         const int a = a0 + lane;
-        int e = -1;
-        if (a < end) e = assignment_expert(p.routes, a, p.K, p.E);
+        const int e = a < end ? src.get(p, a) : -1;
         const bool active = e >= 0;
         const uint64_t peers = match_expert(e, active, p.expert_bits);
         const int leader = peers ? __ffsll((unsigned long long)peers) - 1 : 0;
@@ -291,8 +321,7 @@ __device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int sp
         if (active && lane == leader) off = my[e];
         off = __shfl(off, leader, 64);
         if (active) {
-            const int rank = __popcll(peers & lanemask_lt());
-            p.slots[base[e] + off + rank] = a;
+            p.slots[base[e] + off + __popcll(peers & lanemask_lt())] = a;
             if (lane == leader) my[e] = off + __popcll(peers);
         }
     }
@@ -301,13 +330,13 @@ __device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int sp
 // Padded exclusive scan of total[] over experts into padded[0..E].
 __device__ void padded_scan(const DispatchArgs& p, const DispatchLds& l) {
     const int tid = threadIdx.x;
-    const int per = (p.E + kDispatchThreads - 1) / kDispatchThreads;
+    const int per = (p.E + kThreads - 1) / kThreads;
     const int e0 = tid * per;
     int local = 0;
     for (int e = e0; e < min(p.E, e0 + per); ++e) local += (l.total[e] + p.M - 1) / p.M * p.M;
     l.scan_tmp[tid] = local;
     __syncthreads();
-    for (int d = 1; d < kDispatchThreads; d <<= 1) {
+    for (int d = 1; d < kThreads; d <<= 1) {
         const int v = tid >= d ? l.scan_tmp[tid - d] : 0;
         __syncthreads();
         l.scan_tmp[tid] += v;
@@ -318,7 +347,7 @@ __device__ void padded_scan(const DispatchArgs& p, const DispatchLds& l) {
         l.padded[e] = run;
         run += (l.total[e] + p.M - 1) / p.M * p.M;
     }
-    if (tid == kDispatchThreads - 1) l.padded[p.E] = l.scan_tmp[tid];
+    if (tid == kThreads - 1) l.padded[p.E] = l.scan_tmp[tid];
     __syncthreads();
 }
 
@@ -327,7 +356,7 @@ __device__ void finalize_plan(const DispatchArgs& p, const DispatchLds& l, int s
     const int tid = threadIdx.x;
     const int A = p.tokens * p.K;
     const int padded_total = l.padded[p.E];
-    for (int e = tid; e < p.E; e += kDispatchThreads) {
+    for (int e = tid; e < p.E; e += kThreads) {
         p.meta[e] = l.total[e];
         p.meta[p.E + e] = l.total[e];
         p.offsets[e] = l.padded[e];
@@ -338,7 +367,7 @@ __device__ void finalize_plan(const DispatchArgs& p, const DispatchLds& l, int s
         p.meta[2 * p.E + 1] = padded_total;
     }
     const int ntiles = p.capacity / p.M;
-    for (int tile = tid; tile < ntiles; tile += kDispatchThreads) {
+    for (int tile = tid; tile < ntiles; tile += kThreads) {
         const int row0 = tile * p.M;
         int e = -1;
         if (row0 < padded_total) {
@@ -355,55 +384,80 @@ __device__ void finalize_plan(const DispatchArgs& p, const DispatchLds& l, int s
     }
 }
 
-// One workgroup builds the whole plan.  With `Fused`, the same workgroup
-// first routes every token (decode-sized batches).
-template <bool Fused, int EP>
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_single_kernel(DispatchArgs p) {
+// Routes tokens [t0, t1) with the workgroup (4 tokens per wave per pass),
+// staging the experts of assignments [t0*K, t1*K) in l.eids.
+template <int EP>
+__device__ void route_span(const DispatchArgs& p, const DispatchLds& l, int t0, int t1) {
+    const int row = threadIdx.x >> 4;  // 64 rows per workgroup
+    bool bad = false;
+    for (int tb = t0; tb < t1; tb += kThreads / 16) {
+        const int t = tb + row;
+        const bool active = t < t1;
+        int* eids = l.eids + (size_t)(t - t0) * p.K;
+        if (p.logits_bf16)
+            bad |= route_row<EP, uint16_t>((const uint16_t*)p.logits, t, active, p.routes, p.E, p.K, eids) && active;
+        else
+            bad |= route_row<EP, float>((const float*)p.logits, t, active, p.routes, p.E, p.K, eids) && active;
+    }
+    if (bad) l.flag[0] = 1;
+}
+
+__device__ void clear_counts(const DispatchArgs& p, const DispatchLds& l) {
+    for (int i = threadIdx.x; i < kWaves * p.E; i += kThreads) l.wcount[i] = 0;
+    if (threadIdx.x == 0) l.flag[0] = 0;
+    __syncthreads();
+}
+
+// One workgroup builds the whole plan (optionally routing first).
+template <int EP>
+__global__ __launch_bounds__(kThreads) void dispatch_single_kernel(DispatchArgs p) {
     extern __shared__ int lds[];
     const DispatchLds l = dispatch_lds(lds, p.E);
-    const int wave = threadIdx.x >> 6;
-    if constexpr (Fused) {
-        for (int t = wave; t < p.tokens; t += kDispatchWaves) {
-            if (p.logits_bf16)
-                route_token<EP, uint16_t>(p.logits_bf16 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
-            else
-                route_token<EP, float>(p.logits_f32 + (size_t)t * p.E, p.routes + (size_t)t * 2 * p.K, p.E, p.K);
-        }
-        __threadfence_block();
-        __syncthreads();
-    }
     const int A = p.tokens * p.K;
-    span_counts(p, l, 0, A);
+    clear_counts(p, l);
+    SpanExperts src{nullptr, 0};
+    if (A <= kSpanLds) {
+        if (p.logits) route_span<EP>(p, l, 0, p.tokens);
+        else stage_span(p, l, 0, A);
+        src.lds = l.eids;
+    }
+    __syncthreads();
+    span_counts(p, l, 0, A, src, src.lds == nullptr);
     const int status = l.flag[0];
     padded_scan(p, l);
-    span_scatter(p, l, 0, A, l.padded);
+    span_scatter(p, l, 0, A, src, l.padded);
     finalize_plan(p, l, status);
 }
 
-// Multi-workgroup plan, step 1: per-chunk expert counts and status.
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_hist_kernel(DispatchArgs p) {
+// Multi-workgroup plan, step 1: route (or stage) one chunk of tokens and
+// publish its per-expert counts and status.
+template <int EP>
+__global__ __launch_bounds__(kThreads) void dispatch_hist_kernel(DispatchArgs p) {
     extern __shared__ int lds[];
     const DispatchLds l = dispatch_lds(lds, p.E);
-    const int A = p.tokens * p.K, c = blockIdx.x;
-    const int b = c * p.chunk, e_ = min(A, b + p.chunk);
-    span_counts(p, l, b, e_);
-    for (int e = threadIdx.x; e < p.E; e += kDispatchThreads) p.scratch[(size_t)c * p.E + e] = l.total[e];
+    const int c = blockIdx.x;
+    const int t0 = c * p.chunk_tokens, t1 = min(p.tokens, t0 + p.chunk_tokens);
+    clear_counts(p, l);
+    if (p.logits) route_span<EP>(p, l, t0, t1);
+    else stage_span(p, l, t0 * p.K, t1 * p.K);
+    __syncthreads();
+    span_counts(p, l, t0 * p.K, t1 * p.K, SpanExperts{l.eids, t0 * p.K}, false);
+    for (int e = threadIdx.x; e < p.E; e += kThreads) p.scratch[(size_t)c * p.E + e] = l.total[e];
     if (threadIdx.x == 0) p.scratch[(size_t)gridDim.x * p.E + c] = l.flag[0];
 }
 
 // Step 2 (one workgroup): chunk bases per expert, padded offsets, metadata.
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(DispatchArgs p, int chunks) {
+__global__ __launch_bounds__(kThreads) void dispatch_plan_kernel(DispatchArgs p, int chunks) {
     extern __shared__ int lds[];
     const DispatchLds l = dispatch_lds(lds, p.E);
-    int* cnt = l.scan_tmp + kDispatchThreads;  // [chunks][E]
+    int* cnt = l.eids;  // [chunks][E] <= kPlanLdsWords <= kSpanLds
     const int n = chunks * p.E;
-    for (int i = threadIdx.x; i < n; i += kDispatchThreads) cnt[i] = p.scratch[i];
-    __shared__ int status_word;
-    if (threadIdx.x == 0) status_word = 0;
+    for (int i = threadIdx.x; i < n; i += kThreads) cnt[i] = p.scratch[i];
+    if (threadIdx.x == 0) l.flag[0] = 0;
     __syncthreads();
-    for (int c = threadIdx.x; c < chunks; c += kDispatchThreads)
-        if (p.scratch[(size_t)chunks * p.E + c]) atomicOr(&status_word, 1);
-    for (int e = threadIdx.x; e < p.E; e += kDispatchThreads) {
+    for (int c = threadIdx.x; c < chunks; c += kThreads)
+        if (p.scratch[(size_t)chunks * p.E + c]) l.flag[0] = 1;
+    for (int e = threadIdx.x; e < p.E; e += kThreads) {
         int run = 0;
         for (int c = 0; c < chunks; ++c) {
             const int v = cnt[c * p.E + e];
@@ -413,95 +467,72 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(Dispatc
         l.total[e] = run;
     }
     __syncthreads();
+    const int status = l.flag[0];
     padded_scan(p, l);
-    for (int i = threadIdx.x; i < n; i += kDispatchThreads) p.scratch[i] = cnt[i] + l.padded[i % p.E];
-    finalize_plan(p, l, status_word);
+    for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[i] = cnt[i] + l.padded[i % p.E];
+    finalize_plan(p, l, status);
 }
 
-// Step 3: stable scatter of each chunk from its absolute bases.
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(DispatchArgs p) {
+// Step 3: stable scatter of each chunk from its absolute per-expert bases.
+__global__ __launch_bounds__(kThreads) void dispatch_scatter_kernel(DispatchArgs p) {
     extern __shared__ int lds[];
     const DispatchLds l = dispatch_lds(lds, p.E);
-    const int A = p.tokens * p.K, c = blockIdx.x;
-    const int b = c * p.chunk, e_ = min(A, b + p.chunk);
-    span_counts(p, l, b, e_);
-    span_scatter(p, l, b, e_, p.scratch + (size_t)c * p.E);
-}
-
-// Ordered combine: out[t,h] = bf16(sum_r f32(contrib[t*K + r, h])), ranks in order
-// (moe_dispatch.cuh:13-20); NaN everywhere when the plan was invalid.
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* contributions, uint16_t* output,
-                                                      const int* status, int T_, int H, int K) {
-    const int chunks = H / 8;
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (long)T_ * chunks) return;
-    const int t = (int)(idx / chunks), c = (int)(idx - (long)t * chunks);
-    const bool invalid = status[0] != 0;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const uint16_t* base = contributions + (size_t)t * K * H + c * 8;
-    for (int r = 0; r < K; ++r) {
-        const u32x4 v = *(const u32x4*)(base + (size_t)r * H);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            acc[2 * q] += __uint_as_float(v[q] << 16);
-            acc[2 * q + 1] += __uint_as_float(v[q] & 0xffff0000u);
-        }
-    }
-    u32x4 o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        o[q] = invalid ? 0x7fc07fc0u : pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
-    *(u32x4*)(output + (size_t)t * H + c * 8) = o;
-}
-
-// Scalar combine for hidden sizes that are not multiples of eight.
-__global__ __launch_bounds__(256) void combine_scalar_kernel(const uint16_t* contributions, uint16_t* output,
-                                                             const int* status, int T_, int H, int K) {
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (long)T_ * H) return;
-    const int t = (int)(idx / H), h = (int)(idx - (long)t * H);
-    float acc = 0.f;
-    for (int r = 0; r < K; ++r) acc += bf16_bits_to_float(contributions[((size_t)t * K + r) * H + h]);
-    output[idx] = status[0] ? (uint16_t)0x7fc0 : float_to_bf16_bits(acc);
+    const int c = blockIdx.x;
+    const int b = c * p.chunk_tokens * p.K, e_ = min(p.tokens, (c + 1) * p.chunk_tokens) * p.K;
+    clear_counts(p, l);
+    stage_span(p, l, b, e_);  // routes were validated by the histogram step
+    __syncthreads();
+    const SpanExperts src{l.eids, b};
+    span_counts(p, l, b, e_, src, false);
+    span_scatter(p, l, b, e_, src, p.scratch + (size_t)c * p.E);
 }
 
 template <typename T>
 int launch_route(const T* logits, float* routes, int tokens, int E, int K, hipStream_t s) {
-    const int blocks = (tokens + 3) / 4;
-    const int ep = (E + 63) / 64;
+    const int blocks = (tokens + 15) / 16;
+    const int ep = (E + 15) / 16;
     if (ep <= 1) route_kernel<1, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
     else if (ep <= 2) route_kernel<2, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
     else if (ep <= 4) route_kernel<4, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
     else if (ep <= 8) route_kernel<8, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else route_kernel<16, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 16) route_kernel<16, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
+    else route_kernel<32, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
     return (int)hipGetLastError();
 }
 
-size_t dispatch_lds_bytes(int E) {
-    return sizeof(int) * ((size_t)kDispatchWaves * E + E + E + 1 + 1 + kDispatchThreads);
+template <template <int> class Launch>
+int by_ep(int E, const DispatchArgs& a, unsigned grid, size_t lds, hipStream_t s) {
+    const int ep = (E + 15) / 16;
+    if (ep <= 1) return Launch<1>::go(a, grid, lds, s);
+    if (ep <= 2) return Launch<2>::go(a, grid, lds, s);
+    if (ep <= 4) return Launch<4>::go(a, grid, lds, s);
+    if (ep <= 8) return Launch<8>::go(a, grid, lds, s);
+    if (ep <= 16) return Launch<16>::go(a, grid, lds, s);
+    return Launch<32>::go(a, grid, lds, s);
 }
 
-template <bool Fused>
-int launch_dispatch_single(DispatchArgs a, hipStream_t s) {
-    const size_t lds = dispatch_lds_bytes(a.E);
-    const int ep = (a.E + 63) / 64;
-    if (ep <= 1) dispatch_single_kernel<Fused, 1><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 2) dispatch_single_kernel<Fused, 2><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 4) dispatch_single_kernel<Fused, 4><<<1, kDispatchThreads, lds, s>>>(a);
-    else if (ep <= 8) dispatch_single_kernel<Fused, 8><<<1, kDispatchThreads, lds, s>>>(a);
-    else dispatch_single_kernel<Fused, 16><<<1, kDispatchThreads, lds, s>>>(a);
-    return (int)hipGetLastError();
-}
+template <int EP>
+struct SingleLaunch {
+    static int go(const DispatchArgs& a, unsigned grid, size_t lds, hipStream_t s) {
+        dispatch_single_kernel<EP><<<grid, kThreads, lds, s>>>(a);
+        return (int)hipGetLastError();
+    }
+};
+
+template <int EP>
+struct HistLaunch {
+    static int go(const DispatchArgs& a, unsigned grid, size_t lds, hipStream_t s) {
+        dispatch_hist_kernel<EP><<<grid, kThreads, lds, s>>>(a);
+        return (int)hipGetLastError();
+    }
+};
 
 }  // namespace
 
-// Largest expert count the routing/dispatch kernels accept (8 logits per lane;
-// the dispatch LDS footprint is (18 E + 1026) words, 41 KB at E = 512).
+// Largest expert count the routing/dispatch kernels accept (32 logits per
+// lane of a 16-lane row; dispatch LDS (18 E + 5122) words, 57 KB at E = 512).
 constexpr int kMaxExperts = 512;
 constexpr int kMaxTopK = 32;
-constexpr int kFusedRouteMaxTokens = 256;
-constexpr int kDispatchChunk = 4096;  // assignments per workgroup in the multi-workgroup plan
-constexpr int kPlanLdsWords = 4096;   // [chunks][E] counts staged by the plan workgroup
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M) {
     if (tokens <= 0 || E <= 0 || K <= 0 || M <= 0) return -1;
@@ -519,8 +550,8 @@ int launch_routing(const void* logits, int logits_dtype, float* routes, int toke
     return launch_route<float>((const float*)logits, routes, tokens, E, K, s);
 }
 
-// Dispatch (and, with logits, routing first when the batch is small enough
-// to route inside the dispatch workgroup).
+// Dispatch; with logits, routing runs inside the plan kernels.  `scratch`
+// (optional) enables the multi-workgroup plan for large batches.
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,
                     int* tiles, int tokens, int E, int K, int M, int capacity, void* scratch, size_t scratch_bytes,
                     hipStream_t s) {
@@ -529,7 +560,10 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
         return kInvalid;
     if ((int64_t)tokens * K > (int64_t)1 << 30) return kInvalid;
     if ((int64_t)capacity < capacity_for(tokens, E, K, M)) return kInvalid;
+    if (logits && logits_dtype != 0 && logits_dtype != 1) return kInvalid;
     DispatchArgs a{};
+    a.logits = logits;
+    a.logits_bf16 = logits_dtype == 1;
     a.routes = routes;
     a.meta = meta;
     a.offsets = offsets;
@@ -543,46 +577,30 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
     int bits = 0;
     while ((1 << bits) < E) ++bits;
     a.expert_bits = bits;
-    const int A = tokens * K;
-    // Chunk so that the plan workgroup can stage all [chunks][E] counts in LDS.
-    const int max_chunks = kPlanLdsWords / E;
-    int chunk = kDispatchChunk;
-    if ((A + chunk - 1) / chunk > max_chunks) chunk = ((A + max_chunks - 1) / max_chunks + 1023) / 1024 * 1024;
-    const int chunks = (A + chunk - 1) / chunk;
-    const bool multi = A > kDispatchChunk && scratch && E <= kPlanLdsWords &&
+    const size_t lds = sizeof(int) * dispatch_lds_words(E);
+    a.chunk_tokens = kSpanLds / K / 64 * 64;  // whole 64-token routing passes per chunk
+    if (a.chunk_tokens == 0) a.chunk_tokens = kSpanLds / K;
+    const int chunks = (tokens + a.chunk_tokens - 1) / a.chunk_tokens;
+    const bool multi = chunks > 1 && scratch && (size_t)chunks * E <= (size_t)kPlanLdsWords &&
                        scratch_bytes >= sizeof(int) * ((size_t)chunks * E + chunks);
-    if (logits) {
-        if (logits_dtype != 0 && logits_dtype != 1) return kInvalid;
-        if (tokens <= kFusedRouteMaxTokens && !multi) {
-            if (logits_dtype == 1) a.logits_bf16 = (const uint16_t*)logits;
-            else a.logits_f32 = (const float*)logits;
-            return launch_dispatch_single<true>(a, s);
+    if (!multi) {
+        if (logits && (int64_t)tokens * K > kSpanLds) {  // route separately, plan from routes
+            const int code = launch_routing(logits, logits_dtype, routes, tokens, E, K, s);
+            if (code) return code;
+            a.logits = nullptr;
         }
-        int code = launch_routing(logits, logits_dtype, routes, tokens, E, K, s);
-        if (code) return code;
+        return by_ep<SingleLaunch>(E, a, 1, lds, s);
     }
-    if (!multi) return launch_dispatch_single<false>(a, s);
     a.scratch = (int*)scratch;
-    a.chunk = chunk;
-    const size_t lds = dispatch_lds_bytes(E);
-    dispatch_hist_kernel<<<chunks, kDispatchThreads, lds, s>>>(a);
-    dispatch_plan_kernel<<<1, kDispatchThreads, lds + sizeof(int) * (size_t)chunks * E, s>>>(a, chunks);
-    dispatch_scatter_kernel<<<chunks, kDispatchThreads, lds, s>>>(a);
-    return (int)hipGetLastError();
-}
-
-int launch_combine(const void* contributions, void* output, const int* status, int tokens, int H, int K,
-                   hipStream_t s) {
-    if (!contributions || !output || !status || tokens <= 0 || H <= 0 || K <= 0) return kInvalid;
-    if (H % 8 == 0) {
-        const long n = (long)tokens * (H / 8);
-        combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const uint16_t*)contributions,
-                                                                  (uint16_t*)output, status, tokens, H, K);
-    } else {
-        const long n = (long)tokens * H;
-        combine_scalar_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const uint16_t*)contributions,
-                                                                         (uint16_t*)output, status, tokens, H, K);
+    if (logits) {  // route over the whole GPU, then histogram chunks from the routes
+        const int code = launch_routing(logits, logits_dtype, routes, tokens, E, K, s);
+        if (code) return code;
+        a.logits = nullptr;
     }
+    int code = by_ep<HistLaunch>(E, a, chunks, lds, s);
+    if (code) return code;
+    dispatch_plan_kernel<<<1, kThreads, lds, s>>>(a, chunks);
+    dispatch_scatter_kernel<<<chunks, kThreads, lds, s>>>(a);
     return (int)hipGetLastError();
 }
 

@@ -60,7 +60,7 @@ class SparseMoeConfig:
 @dataclasses.dataclass(frozen=True)
 class MoePrefillTile:
     """Five tile words M,N,K,warps,stages (config.rs:12-20).  M selects the CDNA4
-    row block (16 = weight-streaming kernel, 32/64/128 = LDS-tiled MFMA); the
+    row block (16/32 = weight-streaming kernels, 64/128/256 = LDS-tiled MFMA); the
     remaining words are validated against the reference catalog."""
     m: int = 16
     n: int = 16
@@ -69,10 +69,10 @@ class MoePrefillTile:
     stages: int = 1
 
     def __post_init__(self):
-        ok = (self.m in (16, 32, 64, 128) and self.n in (16, 32, 64, 128) and self.k in (16, 32, 64, 128)
+        ok = (self.m in (16, 32, 64, 128, 256) and self.n in (16, 32, 64, 128) and self.k in (16, 32, 64, 128)
               and self.warps in (1, 2, 4, 8) and self.stages in (1, 2))
         if not ok:
-            raise ValueError(f"unsupported MoE prefill tile {self.values()}; expected M=16|32|64|128, "
+            raise ValueError(f"unsupported MoE prefill tile {self.values()}; expected M=16|32|64|128|256, "
                              "N=16|32|64|128, K=16|32|64|128, warps=1|2|4|8, stages=1|2")
 
     @classmethod

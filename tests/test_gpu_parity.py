@@ -56,7 +56,7 @@ def small_shapes(tau):
 @pytest.mark.parametrize("idx", range(5))
 def test_routing_and_dispatch_bit_exact(tau, oracle, idx):
     name, shape = small_shapes(tau)[idx]
-    for tile_rows in (16, 64, 128):
+    for tile_rows in (16, 32, 64, 128, 256):
         say(f"[routing/dispatch] {name} T={shape.tokens} E={shape.experts} K={shape.top_k} M={tile_rows}")
         layer = tau.inputs.make_layer(shape)
         runner, _ = run_layer(tau, layer, shape, tile_rows)
@@ -86,7 +86,7 @@ def test_layer_matches_oracle(tau, oracle, idx):
     ids, w = oracle.route(lg, shape.top_k)
     ref32 = oracle.moe(x, ids, w, gu, dn)
     ref16 = oracle.moe(x, ids, w, gu, dn, bf16=True)
-    for tile_rows in (16, 32, 64, 128):
+    for tile_rows in (16, 32, 64, 128, 256):
         say(f"[layer] {name} T={shape.tokens} M={tile_rows}")
         _, out = run_layer(tau, layer, shape, tile_rows)
         got = to_np(out)

@@ -1,0 +1,407 @@
+"""GPU tests of the reference-compatible entry points (E=256, K=8) and of the
+shared-expert / single-token paths, modelled on the reference's own tests
+(paths relative to the tau.rs root are cited per test).  Every call goes
+through the C ABI of libtau_moe_hip.so; the oracle is the checker."""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+E, K = 256, 8
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def bf16(a):
+    return torch.tensor(np.asarray(a, np.float32)).to(torch.bfloat16).cuda()
+
+
+def sync_check(code, what):
+    assert code == 0, f"{what} returned {code}"
+    torch.cuda.synchronize()
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def P(t):
+    return None if t is None else t.data_ptr()
+
+
+def S():
+    return torch.cuda.current_stream().cuda_stream
+
+
+# --- routing (crates/models/src/components/cuda/routing.rs:80-160)
+
+def test_routing_matches_sglang_golden_rows(tau):
+    from safetensors.numpy import load_file
+    d = load_file(os.path.join(GOLDEN, "moe_router_sm90.safetensors"))
+    say("[routing] golden SGLang rows")
+    logits = bf16(d["scores"])  # scores are BF16 values promoted losslessly
+    routes = torch.empty(32, 16, device="cuda")
+    sync_check(tau.ffi.lib().tau_launch_moe_routing_fp32(P(logits), P(routes), 32, S()), "routing")
+    out = f32(routes)
+    ids, w = d["ids"].astype(np.int64), d["weights"]
+    np.testing.assert_array_equal(out[:, :8].astype(np.int64), ids)
+    assert np.all(np.abs(out[:, 8:] - w) <= 1e-7 + 1e-5 * np.abs(w))
+    for row in range(32):
+        sel = d["scores"][row, ids[row]].astype(np.float64)
+        ex = np.exp(sel - sel[0])
+        ref = ex / ex.sum()
+        assert np.all(np.abs(out[row, 8:] - ref) <= 1e-7 + 1e-5 * ref)
+
+
+def test_routing_uniform_ties_and_nonfinite_rows(tau):
+    say("[routing] uniform / NaN / inf rows")
+    v = np.zeros((3, 256), np.float32)
+    v[1, 7] = np.nan
+    v[2, 5] = np.inf
+    logits = bf16(v)
+    routes = torch.empty(3, 16, device="cuda")
+    sync_check(tau.ffi.lib().tau_launch_moe_routing_fp32(P(logits), P(routes), 3, S()), "routing")
+    out = f32(routes)
+    assert out[0, :8].tolist() == list(range(8))
+    assert (out[0, 8:] == np.float32(0.125)).all()
+    assert np.isnan(out[1:]).all()
+
+
+# --- dispatch (crates/models/src/components/cuda/fused_moe/prefill/tests.rs:43-120)
+
+@pytest.mark.parametrize("tile_rows", [16, 32, 128])
+def test_dispatch_matches_oracle_with_long_to_short_reuse(tau, oracle, tile_rows):
+    L = tau.ffi.lib()
+    cap = tau.ffi.capacity(257, E, K, tile_rows)
+    meta = torch.zeros(514, dtype=torch.int32, device="cuda")
+    offsets = torch.zeros(257, dtype=torch.int32, device="cuda")
+    slots = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    tiles = torch.zeros(cap // tile_rows, dtype=torch.int32, device="cuda")
+    for tokens in [257, 1, 15, 16, 17, 31, 32, 33, 255, 256, 1]:
+        for concentrated in (False, True):
+            say(f"[dispatch] M={tile_rows} tokens={tokens} concentrated={concentrated}")
+            ids = np.array([[r if concentrated else (t * 8 + r) % 256 for r in range(8)] for t in range(tokens)])
+            routes = np.concatenate([ids.astype(np.float32), np.full((tokens, 8), 0.125, np.float32)], axis=1)
+            r = torch.tensor(routes).cuda()
+            sync_check(L.tau_launch_moe_prefill_dispatch(P(r), P(meta), P(offsets), P(slots), P(tiles), tokens,
+                                                         cap, tile_rows, S()), "dispatch")
+            m, o, s_, t_ = oracle.dispatch(ids, E, tile_rows, cap)
+            np.testing.assert_array_equal(meta.cpu().numpy(), m)
+            np.testing.assert_array_equal(offsets.cpu().numpy(), o)
+            np.testing.assert_array_equal(slots.cpu().numpy(), s_)
+            np.testing.assert_array_equal(tiles.cpu().numpy(), t_)
+
+
+def test_dispatch_rejects_invalid_routes_into_status(tau):
+    say("[dispatch] invalid routes")
+    L = tau.ffi.lib()
+    cap = tau.ffi.capacity(2, E, K, 16)
+    routes = np.zeros((2, 16), np.float32)
+    routes[0, :8] = np.arange(8)
+    routes[1, :8] = [0, 1, 2, 3, 4, 5, 6, 6]  # duplicate expert in a token
+    routes[:, 8:] = 0.125
+    r = torch.tensor(routes).cuda()
+    meta = torch.zeros(514, dtype=torch.int32, device="cuda")
+    offsets = torch.zeros(257, dtype=torch.int32, device="cuda")
+    slots = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    tiles = torch.zeros(cap // 16, dtype=torch.int32, device="cuda")
+    sync_check(L.tau_launch_moe_prefill_dispatch(P(r), P(meta), P(offsets), P(slots), P(tiles), 2, cap, 16, S()),
+               "dispatch")
+    assert int(meta[512]) == 1
+
+
+# --- whole routed prefill vs the oracle (crates/models/src/components/sparse_moe/tests/grouped.rs:7-200)
+
+def reference_generator_layer(tokens, h, i):
+    """The reference's deterministic grouped-prefill inputs (grouped.rs:40-114)."""
+    values = lambda n, seed: (((np.arange(n) * 17 + seed) % 31).astype(np.float32) - 15.) / 128.
+    router = np.zeros((E, h), np.float32)
+    router[:, 0] = np.arange(E) / 32.
+    gate_up = values(E * 2 * i * h, 1).reshape(E, 2 * i, h)
+    down = values(E * h * i, 3).reshape(E, h, i)
+    data = values(tokens * h, 7).reshape(tokens, h)
+    data[:, 0] = np.array([4., -4., 0.])[np.arange(tokens) % 3]
+    logits = data @ router.T  # dyadic operands: exact in f32
+    return data, logits, gate_up, down
+
+
+@pytest.mark.parametrize("h,i", [(33, 17), (144, 80), (272, 272)])
+def test_reference_grouped_prefill_parity(tau, oracle, h, i):
+    toks = [1, 257, 1, 15, 16, 17, 33, 128, 255, 256, 1]
+    L = tau.ffi.lib()
+    gu = bf16(reference_generator_layer(1, h, i)[2])
+    dn = bf16(reference_generator_layer(1, h, i)[3])
+    for m in (16, 32):
+        tile = tau.ffi.TauGemmTile(m, 64 if m == 16 else 32, 64, 4, 2)
+        cap = tau.ffi.capacity(257, E, K, m)
+        ws = dict(
+            routes=torch.empty(257, 16, device="cuda"),
+            meta=torch.empty(514, dtype=torch.int32, device="cuda"),
+            offsets=torch.empty(257, dtype=torch.int32, device="cuda"),
+            slots=torch.empty(cap, dtype=torch.int32, device="cuda"),
+            tiles=torch.empty(cap // m, dtype=torch.int32, device="cuda"),
+            projected=torch.empty(cap, 2 * i, dtype=torch.bfloat16, device="cuda"),
+            activated=torch.empty(cap, i, dtype=torch.bfloat16, device="cuda"),
+            contributions=torch.empty(257 * 8, h, dtype=torch.bfloat16, device="cuda"),
+        )
+        receipts = torch.zeros(10, dtype=torch.int32, device="cuda")
+        for tokens in toks:
+            say(f"[reference prefill] h={h} i={i} M={m} tokens={tokens}")
+            x, logits, _, _ = reference_generator_layer(tokens, h, i)
+            xb, lb = bf16(x), bf16(logits)
+            out = torch.empty(tokens, h, dtype=torch.bfloat16, device="cuda")
+            code = L.tau_launch_moe_prefill(
+                P(xb), P(lb), P(gu), P(dn), P(ws["routes"]), P(ws["meta"]), P(ws["offsets"]), P(ws["slots"]),
+                P(ws["tiles"]), P(ws["projected"]), P(ws["activated"]), P(ws["contributions"]), P(out), tokens, h,
+                i, cap, ctypes.byref(tile), ctypes.byref(tile), P(receipts), S())
+            sync_check(code, "tau_launch_moe_prefill")
+            xf, lf = f32(xb), f32(lb)
+            ids, w = oracle.route(lf, K)
+            np.testing.assert_array_equal(f32(ws["routes"][:tokens, :8]).astype(np.int64), ids)
+            ref16 = oracle.moe(xf, ids, w, f32(gu), f32(dn), bf16=True)
+            ref32 = oracle.moe(xf, ids, w, f32(gu), f32(dn))
+            got = f32(out)
+            e16, e32 = rel_l2(got, ref16), rel_l2(got, ref32)
+            assert e16 <= 2e-3, e16
+            assert e32 <= 1e-2, e32
+            rc = receipts.cpu().tolist()
+            assert rc[0] == m and rc[5] == m  # the requested row block ran in both projections
+    # The generalised entry point with the MFMA row blocks, same inputs.
+    for m in (64, 128, 256):
+        cfg = tau.SparseMoeConfig(h, i, E, K)
+        runner = tau.MoePrefillRunner(cfg, gu, dn, tile_rows=m)
+        for tokens in toks:
+            say(f"[reference prefill _ex] h={h} i={i} M={m} tokens={tokens}")
+            x, logits, _, _ = reference_generator_layer(tokens, h, i)
+            xb, lb = bf16(x), bf16(logits)
+            got = f32(runner.forward(xb, lb))
+            torch.cuda.synchronize()
+            ids, w = oracle.route(f32(lb), K)
+            ref16 = oracle.moe(f32(xb), ids, w, f32(gu), f32(dn), bf16=True)
+            assert rel_l2(got, ref16) <= 2e-3
+            assert runner.executed_tiles()[0][0] == m
+
+
+def test_gate_up_projection_is_exact_on_dyadic_operands(tau, oracle):
+    """Reference gate_up GEMM (moe_gemm.cu, down == 0) on the reference's dyadic
+    generator: every product and partial sum is exact in f32, so the BF16
+    projection must equal the oracle bit for bit at any summation order."""
+    h, i, tokens = 144, 80, 33
+    L = tau.ffi.lib()
+    x, logits, gate_up, down = reference_generator_layer(tokens, h, i)
+    xb, gu = bf16(x), bf16(gate_up)
+    ids, _ = oracle.route(f32(bf16(logits)), K)
+    for m in (16, 32, 64, 128, 256):
+        say(f"[gate_up exact] M={m}")
+        meta, off, slots, tiles = oracle.dispatch(ids, E, m)
+        cap = len(slots)
+        routes = np.concatenate([ids.astype(np.float32), np.full((tokens, 8), 0.125, np.float32)], axis=1)
+        r = torch.tensor(routes).cuda()
+        st = torch.tensor(slots).cuda()
+        tt = torch.tensor(tiles).cuda()
+        out = torch.full((cap, 2 * i), 7.0, dtype=torch.bfloat16, device="cuda")
+        tile = tau.ffi.TauGemmTile(m, 64, 64, 4, 2)
+        receipt = torch.zeros(5, dtype=torch.int32, device="cuda")
+        sync_check(L.tau_launch_moe_prefill_gemm(P(xb), P(gu), P(r), P(st), P(tt), P(out), tokens, cap, 2 * i, h, 0,
+                                                 ctypes.byref(tile), P(receipt), S()), "prefill_gemm")
+        assert int(receipt[0]) == m  # the executed kernel walks the same row blocks as dispatch
+        got = f32(out)
+        gxf, guf = f32(xb), f32(gu)
+        exp = np.zeros((cap, 2 * i), np.float32)
+        for row in range(cap):
+            s_ = slots[row]
+            if s_ < tokens * K:
+                exp[row] = oracle.bf16_round(oracle.linear(gxf[s_ // K][None], guf[ids.reshape(-1)[s_]])[0])
+        np.testing.assert_array_equal(got, exp)
+
+
+def test_down_epilogue_weights_before_the_bf16_round(tau):
+    """linear.rs:176-206: bf16(dot * w) with dot = 1 + 1/256, w = 0.9."""
+    say("[down epilogue] weight before round")
+    L = tau.ffi.lib()
+    tokens, h, i = 1, 2, 2
+    ids = np.arange(8)
+    routes = np.zeros((1, 16), np.float32)
+    routes[0, :8] = ids
+    routes[0, 8] = 0.9
+    a = np.zeros((16, i), np.float32)
+    a[0] = [1.0, 1.0]                                  # row 0 = assignment 0 (expert 0)
+    down = np.zeros((E, h, i), np.float32)
+    down[0, 0] = [1.0, 1.0 / 256.0]
+    slots = np.full(16 * 8, 8, np.int32)
+    tiles = np.full(8, -1, np.int32)
+    for r in range(8):                                 # expert r owns rows [16r, 16r+16)
+        slots[16 * r] = r
+        tiles[r] = r
+    ab = bf16(np.concatenate([a] + [np.zeros((16, i), np.float32)] * 7))
+    out = torch.zeros(8, h, dtype=torch.bfloat16, device="cuda")
+    tile = tau.ffi.TauGemmTile(16, 16, 16, 1, 1)
+    sync_check(L.tau_launch_moe_prefill_gemm(P(ab), P(bf16(down)), P(torch.tensor(routes).cuda()),
+                                             P(torch.tensor(slots).cuda()), P(torch.tensor(tiles).cuda()), P(out),
+                                             tokens, 128, h, i, 1, ctypes.byref(tile), None, S()), "down gemm")
+    got = float(out[0, 0].float())
+    dot = np.float32(1 + 1 / 256)
+    exact = float(torch.tensor(float(dot * np.float32(0.9))).to(torch.bfloat16).float())
+    early = float((torch.tensor(float(dot)).to(torch.bfloat16).float()
+                   * torch.tensor(0.9).to(torch.bfloat16).float()).to(torch.bfloat16).float())
+    assert exact != early
+    assert got == exact
+
+
+def test_nonfinite_logits_fail_closed_then_reset(tau):
+    """prefill/tests.rs:133-165: NaN logits -> all-NaN output; the next valid call
+    on the same workspace is clean."""
+    say("[fail closed]")
+    cfg = tau.SparseMoeConfig(32, 16, E, K)
+    runner = tau.MoePrefillRunner(cfg, torch.zeros(E, 32, 32, dtype=torch.bfloat16, device="cuda"),
+                                  torch.zeros(E, 32, 16, dtype=torch.bfloat16, device="cuda"))
+    x = torch.zeros(1, 32, dtype=torch.bfloat16, device="cuda")
+    bad = torch.full((1, E), float("nan"), device="cuda").to(torch.bfloat16)
+    good = torch.zeros(1, E, dtype=torch.bfloat16, device="cuda")
+    assert torch.isnan(runner.forward(x, bad).float()).all()
+    torch.cuda.synchronize()
+    assert (runner.forward(x, good).float() == 0).all()
+
+
+# --- elementwise entry points
+
+def test_silu_and_mul_entry_point(tau):
+    """silu_and_mul.rs:179-220 vectors: f32 within 1e-5, BF16 within 5e-2."""
+    say("[silu_and_mul]")
+    v = np.array([[1.0, -2.0, 0.5, 3.0, 2.0, 0.25, -4.0, 1.5],
+                  [-0.5, 4.0, -3.0, 2.0, 1.25, -2.0, 0.75, 0.5]], np.float32)
+    t = torch.tensor(v, dtype=torch.float64)
+    ref = (torch.nn.functional.silu(t[:, :4]) * t[:, 4:]).numpy()
+    for dtype, code, tol in [(torch.float32, 0, 1e-5), (torch.bfloat16, 1, 5e-2)]:
+        inp = torch.tensor(v).to(dtype).cuda()
+        out = torch.empty(2, 4, dtype=dtype, device="cuda")
+        sync_check(tau.ffi.lib().tau_launch_silu_and_mul(P(inp), P(out), 2, 4, code, S()), "silu")
+        assert np.abs(f32(out) - ref).max() <= tol
+
+
+@pytest.mark.parametrize("width", [2, 17, 2048])
+def test_shared_combine_matches_scalar_reference(tau, width):
+    """shared_expert.rs:126-176: out == bf16(fma(gate, shared, routed)) with the
+    gate from an f64 dot of the BF16 inputs."""
+    say(f"[shared combine] width={width}")
+    inp = np.zeros(3 * width, np.float32)
+    inp[0], inp[1], inp[2 * width] = 1., 1. / 256., -4.
+    weight = np.zeros(width, np.float32)
+    weight[0] = 1.
+    weight[1 % width] = 1.
+    shared = np.array([((i % 13) - 6.) / 16. for i in range(3 * width)], np.float32)
+    routed = np.array([((i % 17) - 8.) / 32. for i in range(3 * width)], np.float32)
+    tens = [bf16(a.reshape(3, width)) for a in (inp, shared, routed)]
+    wt = bf16(weight)
+    out = torch.empty(3, width, dtype=torch.bfloat16, device="cuda")
+    sync_check(tau.ffi.lib().tau_launch_moe_shared_combine(P(tens[0]), P(wt), P(tens[1]), P(tens[2]), P(out), 3,
+                                                           width, S()), "shared_combine")
+    got = f32(out)
+    xi, s_, r_ = (f32(t).astype(np.float64) for t in tens)
+    for row in range(3):
+        dot = float((xi[row] * f32(wt).astype(np.float64)).sum())
+        gate = np.float64(np.float32(1. / (1. + math.exp(-dot))))
+        fused = (gate * s_[row] + r_[row]).astype(np.float32)  # exact product + sum, one f32 round
+        expected = f32(torch.tensor(fused).to(torch.bfloat16))
+        np.testing.assert_array_equal(got[row], expected)
+
+
+def test_linear_entry_point_exact_on_dyadic_operands(tau):
+    """linear.rs:117-172: f32 projection equals the f64 dot bit for bit."""
+    for rows, cols, inner in [(1, 1, 7), (3, 11, 16), (17, 19, 33), (5, 32, 64), (70, 130, 256)]:
+        say(f"[linear] {rows}x{cols}x{inner}")
+        data = lambda n, seed: np.array([((i * 7 + seed) % 15 - 7) / 16. for i in range(n)], np.float32)
+        x = data(rows * inner, 3).reshape(rows, inner)
+        w = data(cols * inner, 5).reshape(cols, inner)
+        out = torch.empty(rows, cols, device="cuda")
+        sync_check(tau.ffi.lib().tau_launch_linear_bf16_fp32(P(bf16(x)), P(bf16(w)), P(out), rows, cols, inner, S()),
+                   "linear")
+        np.testing.assert_array_equal(f32(out), (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32))
+
+
+def test_decode_gemm_pointer_arrays(tau):
+    """moe_decode_gemm.cu pointer-array GEMV: out[b] = W[b] . x[b] in f32."""
+    say("[decode gemm]")
+    rng = np.random.default_rng(0)
+    batches, cols, inner = 8, 100, 96
+    data = lambda *s: bf16((rng.integers(-7, 8, size=s) / 16.).astype(np.float32))
+    xs = [data(inner) for _ in range(batches)]
+    ws = [data(cols, inner) for _ in range(batches)]
+    outs = [torch.empty(cols, device="cuda") for _ in range(batches)]
+    ptrs = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device="cuda")
+    px, pw, po = ptrs(xs), ptrs(ws), ptrs(outs)
+    prof = tau.ffi.TauDecodeProfile(2, 32, 128, 4, 2)
+    sync_check(tau.ffi.lib().tau_launch_moe_decode_gemm(P(px), P(pw), P(po), batches, cols, inner,
+                                                        ctypes.byref(prof), None, S()), "decode_gemm")
+    for b in range(batches):
+        np.testing.assert_array_equal(f32(outs[b]), (f32(ws[b]).astype(np.float64) @ f32(xs[b]).astype(np.float64))
+                                      .astype(np.float32))
+
+
+def test_fused_single_token_decode(tau, oracle):
+    """fused_bf16_moe_decode.cu:56-91 contract vs the oracle (BF16 contract)."""
+    rng = np.random.default_rng(1)
+    h, i = 256, 64
+    say("[fused decode] one token")
+    x = bf16(rng.standard_normal(h))
+    logits = bf16(rng.standard_normal(E))
+    gu = bf16(rng.standard_normal((E, 2 * i, h)) * 0.05)
+    dn = bf16(rng.standard_normal((E, h, i)) * 0.05)
+    bufs = dict(ids=torch.empty(8, dtype=torch.int32, device="cuda"), w=torch.empty(8, device="cuda"),
+                ptr=torch.empty(64, dtype=torch.int64, device="cuda"),
+                gu_out=torch.empty(8, 2 * i, dtype=torch.bfloat16, device="cuda"),
+                act=torch.empty(8, i, dtype=torch.bfloat16, device="cuda"),
+                eo=torch.empty(8, h, dtype=torch.bfloat16, device="cuda"),
+                gu32=torch.empty(8, 2 * i, device="cuda"), e32=torch.empty(8, h, device="cuda"),
+                out=torch.empty(h, dtype=torch.bfloat16, device="cuda"))
+    prof = tau.ffi.TauDecodeProfile(1, 64, 64, 4, 2)
+    code = tau.ffi.lib().tau_launch_fused_bf16_moe_decode(
+        P(x), P(logits), P(gu), P(dn), P(bufs["ids"]), P(bufs["w"]), P(bufs["ptr"]), P(bufs["gu_out"]),
+        P(bufs["act"]), P(bufs["eo"]), P(bufs["gu32"]), P(bufs["e32"]), P(bufs["out"]), h, i, E, K,
+        ctypes.byref(prof), ctypes.byref(prof), None, S())
+    sync_check(code, "fused decode")
+    ids, w = oracle.route(f32(logits)[None], K)
+    assert bufs["ids"].cpu().tolist() == ids[0].tolist()
+    ref = oracle.moe(f32(x)[None], ids, w, f32(gu), f32(dn), bf16=True)[0]
+    assert rel_l2(f32(bufs["out"]), ref) <= 2e-3
+
+
+def test_shared_expert_path_matches_oracle(tau, oracle):
+    """Routed + gated shared expert (c4-style) vs the oracle's f32 path
+    (shared_expert.rs:39-69,142-160) and its BF16 contract (moe_shared.cu)."""
+    shape = tau.inputs.scaled(tau.inputs.CONFIGS["c4_next_sparse"], 96)
+    say(f"[shared expert] T={shape.tokens}")
+    layer = tau.inputs.make_layer(shape)
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k,
+                              shared_expert=tau.SharedExpertConfig(shape.shared_intermediate))
+    block = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer["shared_gate_up"], layer["shared_down"],
+                               layer["shared_gate"])
+    out = block.forward(layer["x"], layer["logits"])
+    torch.cuda.synchronize()
+    x = f32(layer["x"])
+    ids, w = oracle.route(f32(layer["logits"]), shape.top_k)
+    routed32 = oracle.moe(x, ids, w, f32(layer["gate_up"]), f32(layer["down"]))
+    sh32 = oracle.dense_mlp(x, f32(layer["shared_gate_up"]), f32(layer["shared_down"]))
+    ref32 = oracle.shared_combine_f32(x, f32(layer["shared_gate"]), sh32, routed32)
+    routed16 = oracle.moe(x, ids, w, f32(layer["gate_up"]), f32(layer["down"]), bf16=True)
+    sh16 = oracle.dense_mlp(x, f32(layer["shared_gate_up"]), f32(layer["shared_down"]), bf16=True)
+    ref16 = oracle.shared_combine_bf16(x, f32(layer["shared_gate"]), sh16, routed16)
+    got = f32(out)
+    assert rel_l2(got, ref32) <= 1e-2
+    assert rel_l2(got, ref16) <= 2e-3

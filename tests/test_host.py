@@ -1,0 +1,76 @@
+"""Host-side checks that need no GPU: the C ABI loads and exports every
+declared symbol, launchers reject bad arguments before touching the device,
+and the Python mirror of the reference's config types behaves like it."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "tau_moe.h")).read()
+    return sorted(set(re.findall(r"\b(tau_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(tau):
+    lib = tau.ffi.lib()
+    syms = header_symbols()
+    assert len(syms) >= 20
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(tau.ffi.EXPORTS)
+    assert lib.tau_moe_build_target() == b"gfx950"
+
+
+def test_capacity_and_workspace_queries(tau):
+    assert tau.ffi.capacity(1, 256, 8, 16) == 128  # prefill/tests.rs:127
+    assert tau.moe_prefill_capacity(0) is None
+    assert tau.moe_prefill_capacity(1) == 128
+    sizes = tau.ffi.workspace_bytes(64, 2048, 768, 128, 8, 16)
+    cap = tau.ffi.capacity(64, 128, 8, 16)
+    assert sizes == [64 * 16 * 4, 258 * 4, 129 * 4, cap * 4, cap // 16 * 4, cap * 768 * 2, 64 * 8 * 2048 * 2]
+
+
+def test_launchers_reject_invalid_arguments_without_a_device(tau):
+    L = tau.ffi.lib()
+    null = None
+    assert L.tau_launch_moe_routing_fp32(null, null, 4, null) == 1
+    assert L.tau_launch_moe_prefill_dispatch(null, null, null, null, null, 4, 128, 16, null) == 1
+    assert L.tau_launch_moe_prefill_combine(null, null, null, 1, 8, null) == 1
+    assert L.tau_launch_silu_and_mul(null, null, 1, 1, 1, null) == 1
+    assert L.tau_launch_moe_shared_combine(null, null, null, null, null, 1, 8, null) == 1
+    assert L.tau_launch_linear_bf16_fp32(null, null, null, 1, 1, 1, null) == 1
+    assert L.tau_launch_moe_routing_ex(null, 1, null, 4, 128, 8, null) == 1
+    # fused decode reports argument errors as -1 (fused_bf16_moe_decode.cu:63-66)
+    assert L.tau_launch_fused_bf16_moe_decode(*([null] * 13), 2048, 768, 256, 8, null, null, null, null) == -1
+    # non-null placeholders with invalid shapes are still rejected on the host
+    dummy = ctypes.c_void_p(16)
+    assert L.tau_launch_moe_routing_ex(dummy, 1, dummy, 4, 1025, 8, null) == 1  # E > 512
+    assert L.tau_launch_moe_routing_ex(dummy, 1, dummy, 4, 128, 0, null) == 1
+    assert L.tau_launch_moe_routing_ex(dummy, 1, dummy, 4, 8, 9, null) == 1     # K > E
+    assert L.tau_launch_moe_prefill_dispatch(dummy, dummy, dummy, dummy, dummy, 4, 127, 16, null) == 1  # capacity
+    assert L.tau_moe_prefill_capacity(1, 256, 8, 48) == -1
+
+
+def test_sparse_moe_config_validation_messages(tau):
+    C = tau.SparseMoeConfig
+    C(2, 2, 2, 1, shared_expert=tau.SharedExpertConfig(2)).validate()
+    with pytest.raises(ValueError, match="cannot exceed"):
+        C(2, 2, 2, 3).validate()
+    with pytest.raises(ValueError, match="non-zero"):
+        C(0, 2, 2, 1).validate()
+    with pytest.raises(ValueError, match="shared-expert"):
+        C(2, 2, 2, 1, shared_expert=tau.SharedExpertConfig(0)).validate()
+
+
+def test_prefill_tile_parse_and_validate(tau):
+    T = tau.MoePrefillTile
+    assert T.parse("16,64,64,4,1").values() == [16, 64, 64, 4, 1]
+    assert str(T.parse("32,32,32,2,2")) == "32,32,32,2,2"
+    assert T().values() == [16, 16, 16, 1, 1]
+    for bad in ["16,64,64,4", "16,64,64,4,1,1", "a,b,c,d,e", "24,64,64,4,1", "16,64,64,3,1"]:
+        with pytest.raises(ValueError):
+            T.parse(bad)

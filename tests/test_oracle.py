@@ -1,0 +1,304 @@
+"""CPU checks that pin the oracle (oracle/moe_oracle.c) before it is trusted.
+
+Every check is independent of the oracle's own formulas: golden vectors the
+reference ships, its closed-form unit tests, library routines (torch) for the
+special cases the MoE reduces to, brute-force f64 sums, and invariants.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load_router_fixture():
+    from safetensors.numpy import load_file
+    return load_file(os.path.join(GOLDEN, "moe_router_sm90.safetensors"))
+
+
+# --- routing: golden vectors (crates/models/src/components/cuda/routing.rs:99-160)
+
+def test_router_matches_sglang_golden_rows():
+    d = load_router_fixture()
+    scores, ids_ref, w_ref = d["scores"], d["ids"].astype(np.int64), d["weights"]
+    ids, w = O.route(scores, 8)
+    np.testing.assert_array_equal(ids, ids_ref)
+    assert np.all(np.abs(w - w_ref) <= 1e-7 + 1e-5 * np.abs(w_ref))
+    # Both within the f32 budget of an independent f64 selected softmax.
+    for row in range(scores.shape[0]):
+        sel = scores[row, ids_ref[row]].astype(np.float64)
+        ex = np.exp(sel - sel[0])
+        f64 = ex / ex.sum()
+        assert np.all(np.abs(w[row] - f64) <= 1e-7 + 1e-5 * np.abs(f64))
+
+
+def test_router_fixture_has_eighth_slot_ties_resolved_to_lower_id():
+    d = load_router_fixture()
+    scores, ids_ref = d["scores"], d["ids"].astype(np.int64)
+    ties = 0
+    for row in range(scores.shape[0]):
+        eighth = scores[row, ids_ref[row, 7]]
+        tied = np.nonzero(scores[row] == eighth)[0]
+        outside = [e for e in tied if e not in ids_ref[row]]
+        if outside:  # a tie across the selection boundary
+            ties += 1
+            assert all(e > ids_ref[row, 7] for e in outside)
+    assert ties == 3  # moe_router_sm90.json: "eighth_slot_tie_rows": 3
+
+
+# --- select_experts closed forms (crates/models/src/components/sparse_moe/routing.rs:263-296)
+
+def test_select_experts_tie_break_cases():
+    scores = np.zeros(256, np.float32)
+    for e, v in [(56, 9.), (65, 8.), (99, 7.), (177, 6.), (124, 5.), (132, 4.), (142, 3.), (2, 2.), (102, 2.)]:
+        scores[e] = v
+    assert O.select_experts(scores, 8) == [56, 65, 99, 177, 124, 132, 142, 2]
+    assert O.select_experts(np.ones(256, np.float32), 8) == list(range(8))
+    assert O.select_experts(np.array([1., 2., 2.], np.float32), 3) == [1, 2, 0]
+
+
+def test_select_experts_rejects_nonfinite_and_bad_counts():
+    assert O.select_experts(np.array([np.nan], np.float32), 1) is None
+    assert O.select_experts(np.array([np.inf], np.float32), 1) is None
+    assert O.select_experts(np.array([1.], np.float32), 0) is None
+    assert O.select_experts(np.array([1.], np.float32), 2) is None
+    with pytest.raises(ValueError):
+        O.route(np.array([[0., np.nan]], np.float32), 1)
+
+
+def test_uniform_logits_route_to_first_ids_with_equal_weights():
+    ids, w = O.route(np.zeros((3, 256), np.float32), 8)
+    assert (ids == np.arange(8)).all()
+    assert (w == np.float32(0.125)).all()
+
+
+def test_router_weight_on_feature_zero_closed_form():
+    # crates/models/src/components/sparse_moe/tests/prepared.rs:33-36,136-141:
+    # router row e = e/32 on feature 0 -> input[0] > 0 selects E-1..E-8.
+    E, H = 256, 4
+    router = np.zeros((E, H), np.float32)
+    router[:, 0] = np.arange(E) / 32.
+    x = np.array([[1., 0, 0, 0], [-1., 0, 0, 0], [0., 0, 0, 0]], np.float32)
+    ids, _ = O.route(x @ router.T, 8)
+    assert list(ids[0]) == list(range(E - 1, E - 9, -1))
+    assert list(ids[1]) == list(range(8))
+    assert list(ids[2]) == list(range(8))
+
+
+# --- whole block closed form (crates/models/src/components/sparse_moe/tests/block.rs:4-72)
+
+def test_block_closed_form_individual_and_packed():
+    I2 = np.eye(2, dtype=np.float32)
+    x = np.array([[1., 0.], [0., 1.]], np.float32)
+    ids, w = O.route(x @ I2.T, 1)
+    gate_up = np.stack([np.concatenate([I2, I2]), np.concatenate([I2, I2])])
+    down = np.stack([I2, 2 * I2])
+    routed = O.moe(x, ids, w, gate_up, down, act=O.ACT_RELU)
+    shared = O.dense_mlp(x, np.concatenate([I2, I2]), I2, act=O.ACT_RELU)
+    out = O.shared_combine_f32(x, np.zeros((1, 2), np.float32), shared, routed)
+    assert out.tolist() == [[1.5, 0.0], [0.0, 2.5]]
+
+
+# --- special cases that reduce to library routines (torch, f64)
+
+def _swiglu_torch(x, gate_up, down):
+    x = torch.tensor(x, dtype=torch.float64)
+    gu = torch.tensor(gate_up, dtype=torch.float64)
+    dn = torch.tensor(down, dtype=torch.float64)
+    i = gu.shape[0] // 2
+    g = x @ gu[:i].T
+    u = x @ gu[i:].T
+    return (torch.nn.functional.silu(g) * u) @ dn.T
+
+
+def test_single_expert_is_a_dense_swiglu_mlp():
+    rng = np.random.default_rng(0)
+    T, H, I = 9, 40, 24
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gu = (rng.standard_normal((1, 2 * I, H)) * 0.1).astype(np.float32)
+    dn = (rng.standard_normal((1, H, I)) * 0.1).astype(np.float32)
+    ids, w = O.route(np.zeros((T, 1), np.float32), 1)
+    out = O.moe(x, ids, w, gu, dn)
+    ref = _swiglu_torch(x, gu[0], dn[0]).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_all_experts_selected_is_the_softmax_mixture():
+    rng = np.random.default_rng(1)
+    T, H, I, E = 7, 32, 16, 5
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gu = (rng.standard_normal((E, 2 * I, H)) * 0.1).astype(np.float32)
+    dn = (rng.standard_normal((E, H, I)) * 0.1).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids, w = O.route(logits, E)
+    out = O.moe(x, ids, w, gu, dn)
+    p = torch.softmax(torch.tensor(logits, dtype=torch.float64), dim=-1)
+    ref = sum(p[:, e:e + 1] * _swiglu_torch(x, gu[e], dn[e]) for e in range(E)).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_expert_relabeling_and_token_split_invariance():
+    rng = np.random.default_rng(2)
+    T, H, I, E, K = 12, 24, 8, 6, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gu = (rng.standard_normal((E, 2 * I, H)) * 0.1).astype(np.float32)
+    dn = (rng.standard_normal((E, H, I)) * 0.1).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids, w = O.route(logits, K)
+    out = O.moe(x, ids, w, gu, dn)
+    perm = rng.permutation(E)
+    ids2, w2 = O.route(logits[:, perm], K)
+    out2 = O.moe(x, ids2, w2, gu[perm], dn[perm])
+    np.testing.assert_array_equal(perm[ids2], ids)
+    np.testing.assert_allclose(out2, out, rtol=1e-6, atol=1e-7)
+    half = O.moe(x[:5], ids[:5], w[:5], gu, dn)
+    np.testing.assert_allclose(half, out[:5], rtol=0, atol=0)
+
+
+def test_token_mask_reproduces_rows_exactly():
+    rng = np.random.default_rng(3)
+    T, H, I, E, K = 20, 16, 8, 4, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gu = (rng.standard_normal((E, 2 * I, H)) * 0.1).astype(np.float32)
+    dn = (rng.standard_normal((E, H, I)) * 0.1).astype(np.float32)
+    ids, w = O.route(rng.standard_normal((T, E)).astype(np.float32), K)
+    full = O.moe(x, ids, w, gu, dn)
+    mask = np.zeros(T, np.uint8)
+    mask[[0, 7, 19]] = 1
+    part = O.moe(x, ids, w, gu, dn, token_mask=mask)
+    np.testing.assert_array_equal(part[mask == 1], full[mask == 1])
+
+
+def test_gate_and_up_halves_are_not_interchangeable():
+    # silu(g) * u is not symmetric: swapping the packed halves must change the result.
+    rng = np.random.default_rng(4)
+    T, H, I = 3, 8, 4
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gu = rng.standard_normal((1, 2 * I, H)).astype(np.float32)
+    dn = rng.standard_normal((1, H, I)).astype(np.float32)
+    ids, w = O.route(np.zeros((T, 1), np.float32), 1)
+    a = O.moe(x, ids, w, gu, dn)
+    b = O.moe(x, ids, w, np.concatenate([gu[:, I:], gu[:, :I]], axis=1), dn)
+    assert not np.allclose(a, b)
+    np.testing.assert_allclose(a, _swiglu_torch(x, gu[0], dn[0]).numpy(), rtol=1e-4, atol=1e-5)
+
+
+# --- BF16 contract pieces
+
+def test_dyadic_linear_is_exact():
+    # crates/models/src/components/cuda/linear.rs:117-172 operands.
+    for rows, cols, inner in [(1, 1, 7), (3, 11, 16), (17, 19, 33), (5, 32, 64)]:
+        data = lambda n, seed: np.array([((i * 7 + seed) % 15 - 7) / 16. for i in range(n)], np.float32)
+        x = data(rows * inner, 3).reshape(rows, inner)
+        wt = data(cols * inner, 5).reshape(cols, inner)
+        got = O.linear(x, wt)
+        ref = (x.astype(np.float64) @ wt.astype(np.float64).T).astype(np.float32)
+        np.testing.assert_array_equal(got, ref)
+
+
+def weight_before_round_case():
+    """Two experts, ReLU MLPs: expert 0's down output is exactly 1 + 1/256 (a
+    BF16 halfway case) and expert 1's is zero, so the routed output is
+    bf16(bf16((1 + 1/256) * w0)) (linear.rs:176-206 of the reference)."""
+    x = np.array([[1., 1.]], np.float32)
+    gate_up = np.zeros((2, 4, 2), np.float32)
+    gate_up[:, 0:2, 0] = 1.0  # gate rows read feature 0 -> g = 1
+    gate_up[:, 2:4, 1] = 1.0  # up rows read feature 1 -> u = 1
+    down = np.zeros((2, 2, 2), np.float32)
+    down[0, 0] = [1.0, 1.0 / 256.0]
+    logits = np.array([[math.log(9.0), 0.0]], np.float32)
+    return x, logits, gate_up, down
+
+
+def test_weight_applied_before_bf16_round():
+    x, logits, gate_up, down = weight_before_round_case()
+    ids, w = O.route(logits, 2)
+    assert list(ids[0]) == [0, 1]
+    out = O.moe(x, ids, w, gate_up, down, act=O.ACT_RELU, bf16=True)
+    dot = np.float32(1 + 1 / 256)
+    exact = O.bf16_round(np.float32(dot * w[0, 0]))
+    early = O.bf16_round(O.bf16_round(dot) * O.bf16_round(w[0, 0]))
+    assert exact != early
+    assert out[0, 0] == exact
+
+
+def test_silu_and_mul_fixed_vectors():
+    # crates/models/src/components/cuda/silu_and_mul.rs:183-186
+    v = np.array([[1.0, -2.0, 0.5, 3.0, 2.0, 0.25, -4.0, 1.5],
+                  [-0.5, 4.0, -3.0, 2.0, 1.25, -2.0, 0.75, 0.5]], np.float32)
+    t = torch.tensor(v, dtype=torch.float64)
+    ref = (torch.nn.functional.silu(t[:, :4]) * t[:, 4:]).numpy()
+    np.testing.assert_allclose(O.silu_and_mul(v), ref, atol=1e-5)
+    np.testing.assert_allclose(O.silu_and_mul(v, bf16=True), ref, atol=5e-2)
+
+
+def test_bf16_contract_close_to_f32_path():
+    rng = np.random.default_rng(5)
+    T, H, I, E, K = 16, 64, 32, 8, 2
+    bf = O.bf16_round
+    x = bf(rng.standard_normal((T, H)))
+    gu = bf(rng.standard_normal((E, 2 * I, H)) * 0.05)
+    dn = bf(rng.standard_normal((E, H, I)) * 0.05)
+    ids, w = O.route(bf(rng.standard_normal((T, E))), K)
+    a = O.moe(x, ids, w, gu, dn)
+    b = O.moe(x, ids, w, gu, dn, bf16=True)
+    assert np.array_equal(b, bf(b))
+    assert np.linalg.norm(a - b) / np.linalg.norm(a) < 1e-2
+
+
+# --- dispatch invariants (crates/models/src/components/cuda/fused_moe/prefill/tests.rs:43-127)
+
+@pytest.mark.parametrize("M", [16, 32, 128])
+def test_dispatch_invariants(M):
+    E, K = 256, 8
+    for tokens in [257, 1, 15, 16, 17, 31, 32, 33, 255, 256, 1]:
+        for concentrated in (False, True):
+            ids = np.array([[r if concentrated else (t * 8 + r) % 256 for r in range(K)] for t in range(tokens)])
+            meta, off, slots, tiles = O.dispatch(ids, E, M)
+            cap = len(slots)
+            assert meta[2 * E] == 0
+            assert meta[:E].sum() == tokens * K
+            padded = meta[2 * E + 1]
+            assert padded <= cap and off[E] == padded
+            seen = np.zeros(tokens * K, bool)
+            for e in range(E):
+                assert (off[e + 1] - off[e]) % M == 0
+                assert meta[e] == meta[E + e]
+                prev = -1
+                n = 0
+                for row in range(off[e], off[e + 1]):
+                    assert tiles[row // M] == e
+                    s = slots[row]
+                    if s < tokens * K:
+                        assert not seen[s]
+                        seen[s] = True
+                        assert (s % 8 if concentrated else s % 256) == e
+                        assert s > prev  # stable: token-ascending
+                        prev = s
+                        n += 1
+                    else:
+                        assert s == tokens * K
+                assert n == meta[e]
+            assert seen.all()
+            assert (tiles[padded // M:] == -1).all()
+
+
+def test_capacity_closed_form():
+    # crates/models/src/components/cuda/fused_moe/prefill/tests.rs:123-128
+    assert O.capacity(1, 256, 8, 16) == 128
+    assert O.capacity(0, 256, 8, 16) == -1
+
+
+def test_plan_matches_stable_sort():
+    rng = np.random.default_rng(6)
+    T, E, K = 50, 12, 3
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    counts, off, slots = O.plan(ids, E)
+    order = sorted(range(T * K), key=lambda a: (ids.reshape(-1)[a], a))
+    assert list(slots) == order
+    assert list(counts) == [int((ids == e).sum()) for e in range(E)]
