@@ -179,7 +179,10 @@ def test_reference_grouped_prefill_parity(tau, oracle, h, i):
             got = f32(out)
             e16, e32 = rel_l2(got, ref16), rel_l2(got, ref32)
             assert e16 <= 2e-3, e16
-            assert e32 <= 1e-2, e32
+            # The reference's generator is adversarial for BF16 storage: the
+            # BF16 contract itself sits ~1e-2 from the f32 path at 272x272, so
+            # the kernel may not be further from f32 than the contract is.
+            assert e32 <= max(1e-2, rel_l2(ref16, ref32) + 1e-3), e32
             rc = receipts.cpu().tolist()
             assert rc[0] == m and rc[5] == m  # the requested row block ran in both projections
     # The generalised entry point with the MFMA row blocks, same inputs.
@@ -252,8 +255,9 @@ def test_down_epilogue_weights_before_the_bf16_round(tau):
     ab = bf16(np.concatenate([a] + [np.zeros((16, i), np.float32)] * 7))
     out = torch.zeros(8, h, dtype=torch.bfloat16, device="cuda")
     tile = tau.ffi.TauGemmTile(16, 16, 16, 1, 1)
-    sync_check(L.tau_launch_moe_prefill_gemm(P(ab), P(bf16(down)), P(torch.tensor(routes).cuda()),
-                                             P(torch.tensor(slots).cuda()), P(torch.tensor(tiles).cuda()), P(out),
+    # Keep every device buffer referenced until the launch has completed.
+    db, rt, st, tt = bf16(down), torch.tensor(routes).cuda(), torch.tensor(slots).cuda(), torch.tensor(tiles).cuda()
+    sync_check(L.tau_launch_moe_prefill_gemm(P(ab), P(db), P(rt), P(st), P(tt), P(out),
                                              tokens, 128, h, i, 1, ctypes.byref(tile), None, S()), "down gemm")
     got = float(out[0, 0].float())
     dot = np.float32(1 + 1 / 256)
@@ -330,7 +334,8 @@ def test_linear_entry_point_exact_on_dyadic_operands(tau):
         x = data(rows * inner, 3).reshape(rows, inner)
         w = data(cols * inner, 5).reshape(cols, inner)
         out = torch.empty(rows, cols, device="cuda")
-        sync_check(tau.ffi.lib().tau_launch_linear_bf16_fp32(P(bf16(x)), P(bf16(w)), P(out), rows, cols, inner, S()),
+        xb, wb = bf16(x), bf16(w)
+        sync_check(tau.ffi.lib().tau_launch_linear_bf16_fp32(P(xb), P(wb), P(out), rows, cols, inner, S()),
                    "linear")
         np.testing.assert_array_equal(f32(out), (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32))
 
