@@ -302,3 +302,21 @@ def test_plan_matches_stable_sort():
     order = sorted(range(T * K), key=lambda a: (ids.reshape(-1)[a], a))
     assert list(slots) == order
     assert list(counts) == [int((ids == e).sum()) for e in range(E)]
+
+
+@pytest.mark.parametrize("width", [2, 17, 2048])
+def test_shared_combine_bf16_against_f64_scalar_gate(width):
+    # crates/models/src/components/cuda/shared_expert.rs:126-176 vectors.
+    inp = np.zeros((3, width), np.float32)
+    inp[0, 0], inp[0, 1], inp[2, 0] = 1., 1. / 256., -4.
+    weight = np.zeros(width, np.float32)
+    weight[0] = 1.
+    weight[1 % width] = 1.
+    shared = O.bf16_round(np.array([((i % 13) - 6.) / 16. for i in range(3 * width)], np.float32)).reshape(3, width)
+    routed = O.bf16_round(np.array([((i % 17) - 8.) / 32. for i in range(3 * width)], np.float32)).reshape(3, width)
+    got = O.shared_combine_bf16(inp, weight, shared, routed)
+    for row in range(3):
+        dot = float((inp[row].astype(np.float64) * weight).sum())
+        gate = np.float64(np.float32(1. / (1. + math.exp(-dot))))
+        exp = O.bf16_round((gate * shared[row] + routed[row]).astype(np.float32))
+        np.testing.assert_array_equal(got[row], exp)
