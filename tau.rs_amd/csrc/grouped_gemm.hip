@@ -682,6 +682,15 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     }
     __syncthreads();
 
+    // A wave whose rows are all padding (an expert's tail block) skips its
+    // fragment reads and MFMAs; it still loads its share and joins barriers.
+    bool wave_rows_live = true;
+    if constexpr (AM == kAGather || EPI == kEpiScatterWeighted) {
+        bool any = false;
+        for (int j = lane; j < TM; j += 64) any |= row_src[wm * TM + j] >= 0;
+        wave_rows_live = __any(any);
+    }
+
     // Per-lane load sources.  Instruction i of wave w fills rows
     // [q*RPI, (q+1)*RPI) with q = i*(NT/64) + w; lane l supplies row
     // q*RPI + l/CPR into chunk slot l%CPR, i.e. global chunk slot ^ swz(row).
@@ -818,6 +827,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             if (kt + PD < nk) prefetch(kt + PD);
         const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
         const uint16_t* Bs = As + BM * BK;
+        if (!wave_rows_live) continue;
         bf16x8 af[2][MI], bfr[2][NI];
         frags(As, Bs, 0, af[0], bfr[0]);
 #pragma unroll

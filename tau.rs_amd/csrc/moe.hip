@@ -109,9 +109,11 @@ int tau_moe_select_tile_rows(int tokens, int experts, int top_k, int hidden, int
     (void)intermediate;
     if (tokens <= 0 || experts <= 0 || top_k <= 0) return 16;
     const double rows_per_expert = (double)tokens * top_k / experts;
+    // Decode-sized groups stream weights; anything larger uses 256-row MFMA
+    // tiles, whose all-padding wave rows skip their MFMAs, so skewed routing
+    // (few hot experts) and balanced routing both keep the weight panels in
+    // as few tiles as possible.
     if (rows_per_expert <= 16.0) return 16;
-    if (rows_per_expert <= 96.0) return 64;
-    if (rows_per_expert <= 384.0) return 128;
     return 256;
 }
 
