@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--banks", type=int, default=0, help="weight banks to rotate (0 = auto)")
     ap.add_argument("--tile-rows", type=int, default=0, help="override the library's row-block choice")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
 
@@ -140,6 +142,32 @@ def cpu_baseline(layer, seconds):
     }
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch (fetch + write) recorded from rocprofv3 --pmc runs
+    in profiles/hbm_traffic.txt, or None when not measured for this case."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        parts = line.split()
+        if len(parts) == 4 and not line.startswith("#") and parts[0] == workload and parts[1] == kernel:
+            return int(parts[2]) + int(parts[3])
+    return None
+
+
+def copy_calibration(torch):
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -149,6 +177,9 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
     tau = load_package()
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
@@ -214,7 +245,7 @@ def main():
         },
         "roofline": {
             "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": None,
+            "frac": achieved / peak, "traffic": measured_traffic(shape.name, dominant),
             "kernel_ms": {"gate_up": ms_gu, "down": ms_dn},
             "algorithmic_per_launch": {"gate_up": traffic_alg[0], "down": traffic_alg[1]},
         },
