@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--banks", type=int, default=0, help="weight banks to rotate (0 = auto)")
     ap.add_argument("--tile-rows", type=int, default=0, help="override the library's row-block choice")
+    ap.add_argument("--weight-layout", choices=("auto", "row_major", "frag16"), default="auto",
+                    help="expert weight layout held by the runner (auto: FRAG16 when the shape allows)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
@@ -66,14 +68,18 @@ def parse():
 class Layer:
     """One workload: inputs, rotating weight banks and a dispatch workspace."""
 
-    def __init__(self, tau, torch, shape, banks, tile_rows=0):
+    def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto"):
         self.tau, self.torch, self.shape = tau, torch, shape
         self.data = tau.inputs.make_layer(shape)
-        self.banks = [(self.data["gate_up"], self.data["down"])]
-        for _ in range(banks - 1):
-            self.banks.append((self.data["gate_up"].clone(), self.data["down"].clone()))
         cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
-        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"], tile_rows=tile_rows or None)
+        # The runner prepares the weights once (load time): FRAG16 copies when
+        # the shape allows, as a serving deployment would hold them.
+        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"], tile_rows=tile_rows or None,
+                                           weight_layout=weight_layout)
+        self.layout = self.runner.layout
+        self.banks = [(self.runner.gate_up, self.runner.down)]
+        for _ in range(banks - 1):
+            self.banks.append((self.runner.gate_up.clone(), self.runner.down.clone()))
         self.tile_rows = self.runner.tile_rows_for(shape.tokens)
         self.ws = self.runner.workspace(shape.tokens, self.tile_rows)
         self.out = torch.empty_like(self.data["x"])
@@ -83,7 +89,7 @@ class Layer:
         gu, dn = self.banks[i % len(self.banks)]
         s = self.shape
         self.tau.ffi.prefill_ex(self.data["x"], self.data["logits"], gu, dn, self.ws, self.out, s.experts,
-                                s.top_k, self.tile_rows, receipts=self.receipts)
+                                s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout)
 
     def projection(self, i, which):
         gu, dn = self.banks[i % len(self.banks)]
@@ -93,7 +99,7 @@ class Layer:
         else:
             a, w, out = self.ws["activated"], dn, self.ws["contributions"]
         self.tau.ffi.grouped_gemm_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, s.experts, s.top_k,
-                                     self.tile_rows, which)
+                                     self.tile_rows, which, weight_layout=self.layout)
 
 
 def time_events(torch, fn, n):
@@ -145,14 +151,17 @@ def cpu_baseline(layer, seconds):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
 
 
-def measured_traffic(workload, kernel):
+def measured_traffic(workload, kernel, layout):
     """HBM bytes per launch (fetch + write) recorded from rocprofv3 --pmc runs
-    in profiles/hbm_traffic.txt, or None when not measured for this case."""
+    in profiles/hbm_traffic.txt (lines: workload kernel fetch write layout), or
+    None when not measured for this case."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     for line in open(TRAFFIC_FILE):
         parts = line.split()
-        if len(parts) == 4 and not line.startswith("#") and parts[0] == workload and parts[1] == kernel:
+        if line.startswith("#") or len(parts) != 5:
+            continue
+        if parts[0] == workload and parts[1] == kernel and parts[4] == layout:
             return int(parts[2]) + int(parts[3])
     return None
 
@@ -184,7 +193,7 @@ def main():
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
-    layer = Layer(tau, torch, shape, banks, args.tile_rows)
+    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout)
 
     for i in range(args.warmup):
         layer.step(i)
@@ -225,6 +234,7 @@ def main():
     tokens_per_s = T / (ms_step * 1e-3)
     layer_hbm = bytes_ / (ms_step * 1e-3) / 1e9
     layer_mfma = flops / (ms_step * 1e-3) / 1e12
+    layout_name = "frag16" if layer.layout == tau.ffi.WEIGHTS_FRAG16 else "row_major"
     result = {
         "metric": "MoE-layer tokens/s; % bf16 MFMA peak (prefill), % HBM BW (decode)",
         "value": tokens_per_s,
@@ -241,11 +251,12 @@ def main():
         "config": {
             "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
+            "weight_layout": layout_name,
             "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
         "roofline": {
             "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": measured_traffic(shape.name, dominant),
+            "frac": achieved / peak, "traffic": measured_traffic(shape.name, dominant, layout_name),
             "kernel_ms": {"gate_up": ms_gu, "down": ms_dn},
             "algorithmic_per_launch": {"gate_up": traffic_alg[0], "down": traffic_alg[1]},
         },

@@ -35,6 +35,18 @@
 extern "C" {
 #endif
 
+/* Expert weight layouts accepted by the *_ex entry points.
+ *   ROW_MAJOR: W[e][n][k] as the reference stores it (gate_up [E,2I,H],
+ *              down [E,H,I]).
+ *   FRAG16:    the same values regrouped by tau_moe_pack_weights into 1 KB
+ *              MFMA operand fragments: 16-byte piece p of expert e holds row
+ *              16*b + (p%64)%16, columns 32*c + 8*((p%64)/16) .. +8, where
+ *              p = (b*(k/32) + c)*64 + lane.  Needs n % 16 == 0 and
+ *              k % 64 == 0; every weight stream then reads whole 1 KB
+ *              contiguous fragments. */
+#define TAU_MOE_WEIGHTS_ROW_MAJOR 0
+#define TAU_MOE_WEIGHTS_FRAG16 1
+
 /* repr(C) tile words of crates/cuda-kernels/src/moe/config.rs:12-20. */
 typedef struct TauGemmTile { int m, n, k, warps, stages; } TauGemmTile;
 /* repr(C) profile words of crates/cuda-kernels/src/moe/decode_config.rs:10-18. */
@@ -144,12 +156,13 @@ int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, c
 
 /* Whole routed path for any (E, K): routing, dispatch, gate_up+SiLU·mul,
  * down+weight, combine.  tile_rows from tau_moe_select_tile_rows (or any of
- * 16/32/64/128/256); receipts (optional) receive 10 words, gate_up then down. */
+ * 16/32/64/128/256); weight_layout TAU_MOE_WEIGHTS_* for both weight tensors;
+ * receipts (optional) receive 10 words, gate_up then down. */
 int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_dtype, const void* gate_up,
                               const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                               void* activated, void* contributions, void* output, int tokens, int hidden,
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                              int* receipts, void* stream);
+                              int weight_layout, int* receipts, void* stream);
 
 /* One grouped projection over an existing dispatch (meta/slots/tiles from
  * tau_launch_moe_prefill_dispatch_ex with the same tile_rows):
@@ -160,7 +173,7 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
 int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* routes, const int* slots,
                                    const int* tiles, const int* meta, void* out, int tokens, int hidden,
                                    int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                                   int projection, int* receipt, void* stream);
+                                   int projection, int weight_layout, int* receipt, void* stream);
 
 /* Always-on shared expert (shared_expert.rs:39-69): dense gated MLP over all
  * tokens with gate_up_s BF16 [2Is,H], down_s BF16 [Is,H]^T = [H,Is], then
@@ -170,7 +183,13 @@ int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* ro
 int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, const void* down_s,
                                     const void* gate_weight, const void* routed, void* activated_ws,
                                     void* shared_ws, void* output, int tokens, int hidden,
-                                    int shared_intermediate, void* stream);
+                                    int shared_intermediate, int weight_layout, void* stream);
+
+/* Load-time weight preparation (no reference counterpart: the reference's
+ * kernels read its packed [E, n, k] storage directly, sparse_moe/experts.rs:
+ * 50-90).  Writes the FRAG16 form of row-major src [experts, rows, columns]
+ * into dst (same size, must not overlap).  rows % 16 == 0, columns % 64 == 0. */
+int tau_moe_pack_weights(const void* src, void* dst, int experts, int rows, int columns, void* stream);
 
 /* Library identification: gfx target the code objects were built for. */
 const char* tau_moe_build_target(void);

@@ -59,7 +59,35 @@ __global__ __launch_bounds__(256) void shared_combine_kernel(const uint16_t* x, 
             fmaf(gate, bf16_bits_to_float(shared[row + c]), bf16_bits_to_float(routed[row + c])));
 }
 
+// Row-major W[e][rows][cols] -> frag16: 16-byte piece p of the output holds
+// row 16*band + lane%16, columns 32*kc + 8*(lane/16) .. +8, where
+// p = ((e*bands + band)*kchunks + kc)*64 + lane.  One thread per piece; the
+// writes are fully coalesced, the reads are 16-byte segments of 16 rows.
+__global__ void pack_frag16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows,
+                                   int cols, long pieces) {
+    const int kchunks = cols / 32, bands = rows / 16;
+    for (long p = blockIdx.x * (long)blockDim.x + threadIdx.x; p < pieces; p += (long)gridDim.x * blockDim.x) {
+        const int lane = (int)(p & 63);
+        const long f = p >> 6;
+        const int kc = (int)(f % kchunks);
+        const long eb = f / kchunks;
+        const int band = (int)(eb % bands);
+        const long e = eb / bands;
+        const long row = (long)band * 16 + (lane & 15);
+        const long col = (long)kc * 32 + (lane >> 4) * 8;
+        *(u32x4*)(dst + p * 8) = *(const u32x4*)(src + (e * rows + row) * cols + col);
+    }
+}
+
 }  // namespace
+
+int launch_pack_frag16(const void* src, void* dst, int experts, int rows, int cols, hipStream_t s) {
+    const long pieces = (long)experts * rows * cols / 8;
+    long blocks = (pieces + 255) / 256;
+    if (blocks > 65535L * 8) blocks = 65535L * 8;
+    pack_frag16_kernel<<<(unsigned)blocks, 256, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, rows, cols, pieces);
+    return (int)hipGetLastError();
+}
 
 int launch_silu_and_mul(const void* in, void* out, int rows, int columns, int dtype, hipStream_t s) {
     if (!in || !out || rows <= 0 || columns <= 0 || (dtype != 0 && dtype != 1)) return kInvalid;

@@ -399,7 +399,7 @@ struct StreamBatch {
 };
 
 // RT 16-row token groups share every weight fragment (rows per item = 16*RT).
-template <int AM, int EPI, int NB, int U, int W, int RT>
+template <int AM, int EPI, int NB, int U, int W, int RT, int WL = kWeightsRowMajor>
 __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
     constexpr bool kSilu = EPI == kEpiSilu;
     constexpr int R = 16 * RT;
@@ -449,8 +449,12 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int col = ng * 16 * NB + b * 16 + (lane & 15);
-        wg[b] = wexp + (long)(col < p.n ? col : 0) * p.k + kofs;
+        if constexpr (WL == kWeightsFrag16)  // 1 KB fragment per 32-wide K chunk, lanes in MFMA order
+            wg[b] = wexp + (long)(col < p.n ? col >> 4 : 0) * 16 * p.k + lane * 8;
+        else
+            wg[b] = wexp + (long)(col < p.n ? col : 0) * p.k + kofs;
     }
+    constexpr int KS = WL == kWeightsFrag16 ? 16 : 1;  // weight elements per unit of k
     const long up = (long)p.w_up_offset * p.k;
 
     f32x4 acc_g[NB][RT], acc_u[NB][RT];
@@ -466,8 +470,8 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
         for (int q = 0; q < U; ++q) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                t.g[b][q] = *(const u32x4*)(wg[b] + kb + q * 32);
-                if constexpr (kSilu) t.u[b][q] = *(const u32x4*)(wg[b] + up + kb + q * 32);
+                t.g[b][q] = *(const u32x4*)(wg[b] + (kb + q * 32) * KS);
+                if constexpr (kSilu) t.u[b][q] = *(const u32x4*)(wg[b] + up + (kb + q * 32) * KS);
             }
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) t.x[rt][q] = *(const u32x4*)(xs[rt] + kb + q * 32);
@@ -520,8 +524,8 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
             for (int b = 0; b < NB; ++b) {
                 u32x4 gv = {0u, 0u, 0u, 0u}, uv = {0u, 0u, 0u, 0u};
                 if (in) {
-                    gv = *(const u32x4*)(wg[b] + kb);
-                    if constexpr (kSilu) uv = *(const u32x4*)(wg[b] + up + kb);
+                    gv = *(const u32x4*)(wg[b] + kb * KS);
+                    if constexpr (kSilu) uv = *(const u32x4*)(wg[b] + up + kb * KS);
                 }
                 acc_g[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(gv), as_bf16x8(xv), acc_g[b][rt], 0, 0, 0);
                 if constexpr (kSilu)
@@ -582,10 +586,12 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
 // Direct-to-LDS pipelined MFMA kernel (prefill, K a multiple of 64)
 // ---------------------------------------------------------------------------
 // Block tile BM x BN x 64; WM x WN waves, each owning a (BM/WM) x (BN/WN) grid
-// of 32x32x16 MFMAs.  Operand panels move HBM -> LDS with global_load_lds
-// (16 bytes per lane, no VGPR staging) into STAGES ring buffers; rows are 128
-// bytes with the 16-byte chunk index XOR-swizzled by (row & 7), so the
-// fragment reads (32 rows x 16 bytes per half-wave) spread over all banks.
+// of 32x32x16 MFMAs.  Operand panels move HBM -> LDS with direct-to-LDS loads
+// (16 bytes per lane, no VGPR staging) into STAGES ring buffers.  A rows (and
+// row-major weight rows) are 128 bytes with the 16-byte chunk index XOR-
+// swizzled (swz below), so fragment reads spread over all banks; frag16
+// weights are staged as whole 1 KB fragments, whose 16-lane read phases are
+// 256 contiguous bytes.
 // One barrier per K step: waiting on the oldest stage's loads, the barrier,
 // then the next loads into the stage every wave has just finished with.
 // The epilogue stages the BF16 tile in LDS and writes 16-byte row segments,
@@ -595,6 +601,24 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+
+// One 16-byte-per-lane global -> LDS copy; the wave's 64 lanes fill 1 KB of
+// LDS from `lds` on.  Issued as inline assembly so that the compiler's
+// wait-count insertion does not track it: the builtin form makes every later
+// LDS read wait for all outstanding copies (vmcnt(0)), including the ones for
+// the stage after next, which serialises loads with MFMAs.  Completion is
+// awaited explicitly with wait_vmcnt before the barrier that publishes a stage.
+__device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds) {
+    typedef __attribute__((address_space(3))) uint16_t* lds_u16;
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u16)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which waits
+// for every outstanding global load, in-flight LDS copies included).  Callers
+// order LDS themselves: copies by wait_vmcnt, fragment reads are consumed by
+// MFMAs (lgkmcnt) before the barrier that lets a stage be overwritten.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // XOR swizzle of the 16-byte chunk slot within a staged row.  LDS has 64
 // banks of 4 bytes (256 bytes); a 16-lane phase of a fragment read touches 16
@@ -608,7 +632,7 @@ __device__ __forceinline__ int swz(int row) {
     else return (row >> 2) & 3;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int PD = 0>
+template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int WL = kWeightsRowMajor>
 __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     constexpr int NT = 64 * WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
@@ -628,8 +652,6 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM_ELEMS];
     __shared__ long row_src[BM];   // gather: source row of A; down: destination slot (or -1)
     __shared__ float row_w[BM];    // down: route weight
-    __shared__ uint32_t junk[WM * WN * 64];  // landing area of the L2 prefetches
-    static_assert(PD == 0 || STAGES == 2, "L2 prefetch is scheduled for two stages");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -710,65 +732,41 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         a_src[i] = p.a + src_row * (long)p.lda + kchunk;
     }
     const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
+    // Weight row of the B tile's row r (gate rows first, then up rows, for SiLU).
+    auto weight_row = [&](int r) -> long {
+        if constexpr (EPI == kEpiSilu) {
+            const int j = c0 + (r < BN / 2 ? r : r - BN / 2);
+            return j < p.n ? (r < BN / 2 ? j : j + p.w_up_offset) : 0;
+        } else {
+            const int j = c0 + r;
+            return j < p.n ? j : 0;
+        }
+    };
+    // Row-major weights: staged like A (swizzled 128-byte rows).  Frag16
+    // weights: instruction q copies one whole 1 KB fragment (16 rows x 32 of
+    // K), so the B stage holds BN/16 bands x BK/32 fragments in global order.
     const uint16_t* b_src[BCH];
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
-        const int r = (i * (NT / 64) + wave) * RPI + lrow8;
-        const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
-        long wrow;
-        if constexpr (EPI == kEpiSilu) {
-            const int j = c0 + (r < BN / 2 ? r : r - BN / 2);
-            wrow = j < p.n ? (r < BN / 2 ? j : j + p.w_up_offset) : 0;
+        const int q = i * (NT / 64) + wave;
+        if constexpr (WL == kWeightsFrag16) {
+            const int band = q / (BK / 32), c = q % (BK / 32);
+            b_src[i] = wexp + (weight_row(band * 16) >> 4) * 16L * p.k + c * 512 + lane * 8;
         } else {
-            const int j = c0 + r;
-            wrow = j < p.n ? j : 0;
-        }
-        b_src[i] = wexp + wrow * (long)p.k + kchunk;
-    }
-
-    // L2 prefetch: thread t < BM + BN touches one 128-byte line of staged row t
-    // PD K-tiles ahead (4-byte global_load_lds into `junk`), so HBM sees more
-    // bytes in flight than the LDS stages alone can hold.
-    constexpr int PF_ROWS = BM + BN;
-    constexpr int PF_WAVES = (PF_ROWS + 63) / 64;  // waves that issue a prefetch
-    const uint16_t* pf_src = nullptr;
-    if constexpr (PD > 0) {
-        const int r = tid < PF_ROWS ? tid : 0;
-        if (r < BM) {
-            long src_row;
-            if constexpr (AM == kAGather) src_row = row_src[r] >= 0 ? row_src[r] : 0;
-            else src_row = row0 + r < p.rows ? row0 + r : 0;
-            pf_src = p.a + src_row * (long)p.lda;
-        } else {
-            const int rb = r - BM;
-            long wrow;
-            if constexpr (EPI == kEpiSilu) {
-                const int j = c0 + (rb < BN / 2 ? rb : rb - BN / 2);
-                wrow = j < p.n ? (rb < BN / 2 ? j : j + p.w_up_offset) : 0;
-            } else {
-                const int j = c0 + rb;
-                wrow = j < p.n ? j : 0;
-            }
-            pf_src = wexp + wrow * (long)p.k;
+            const int r = q * RPI + lrow8;
+            const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
+            b_src[i] = wexp + weight_row(r) * (long)p.k + kchunk;
         }
     }
-    typedef __attribute__((address_space(3))) void* lds_ptr;
-    auto prefetch = [&](int kt) {
-        if (wave < PF_WAVES)
-            __builtin_amdgcn_global_load_lds((const void*)(pf_src + kt * BK), (lds_ptr)(junk + wave * 64), 4, 0, 0);
-    };
     auto issue = [&](int kt, int stage) {
         uint16_t* As = smem + stage * STAGE_ELEMS;
         uint16_t* Bs = As + BM * BK;
         const int kb = kt * BK;
 #pragma unroll
-        for (int i = 0; i < ACH; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + kb),
-                                             (lds_ptr)(As + (i * (NT / 64) + wave) * 512), 16, 0, 0);
+        for (int i = 0; i < ACH; ++i) lds_dma16(a_src[i] + kb, As + (i * (NT / 64) + wave) * 512);
 #pragma unroll
         for (int i = 0; i < BCH; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(b_src[i] + kb),
-                                             (lds_ptr)(Bs + (i * (NT / 64) + wave) * 512), 16, 0, 0);
+            lds_dma16(b_src[i] + (WL == kWeightsFrag16 ? kb * 16 : kb), Bs + (i * (NT / 64) + wave) * 512);
     };
 
     f32x16 acc[MI][NI];
@@ -783,8 +781,6 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
 #pragma unroll
     for (int s_ = 0; s_ < STAGES - 1; ++s_)
         if (s_ < nk) issue(s_, s_);
-    if constexpr (PD > 0)
-        for (int d = 1; d < PD && d < nk; ++d) prefetch(d);
 
     const int lr = lane & 31, lh = lane >> 5;
     // Fragment reads of one 16-deep K step; the next step's reads are issued
@@ -805,26 +801,24 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             } else {
                 r = wn * TN + j * 32 + lr;
             }
-            bfr[j] = as_bf16x8(*(const u32x4*)(Bs + r * BK + ((c ^ swz<CPR>(r)) * 8)));
+            if constexpr (WL == kWeightsFrag16) {
+                // row r, K piece 2*ks + lh of the stage: fragment (r/16, piece/4),
+                // 16-byte slot (piece%4)*16 + r%16.
+                const int piece = ks * 2 + lh;
+                bfr[j] = as_bf16x8(*(const u32x4*)(Bs + ((r >> 4) * (BK / 32) + (piece >> 2)) * 512 +
+                                                   ((piece & 3) * 16 + (r & 15)) * 8));
+            } else {
+                bfr[j] = as_bf16x8(*(const u32x4*)(Bs + r * BK + ((c ^ swz<CPR>(r)) * 8)));
+            }
         }
     };
     for (int kt = 0; kt < nk; ++kt) {
         // Tile kt's loads are done once at most the later-issued loads remain
         // (VMEM loads complete in order).
-        if constexpr (PD > 0) {
-            // Issued after tile kt's stage: the prefetch(es) of the previous
-            // iteration (or of the prologue for kt == 0), by prefetching waves.
-            if (wave < PF_WAVES && kt > 0 && kt - 1 + PD < nk) wait_vmcnt<1>();
-            else if (wave < PF_WAVES && kt == 0 && PD == 2 && nk > 1) wait_vmcnt<1>();
-            else wait_vmcnt<0>();
-        } else {
-            if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
-            else wait_vmcnt<0>();
-        }
-        __syncthreads();
+        if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
+        else wait_vmcnt<0>();
+        lds_barrier();
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        if constexpr (PD > 0)
-            if (kt + PD < nk) prefetch(kt + PD);
         const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
         const uint16_t* Bs = As + BM * BK;
         if (!wave_rows_live) continue;
@@ -896,14 +890,14 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int PD = 0>
+template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int WL = kWeightsRowMajor>
 int launch_mfma(const GemmArgs& p, hipStream_t s) {
     constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
     const long m_blocks = (p.rows + BM - 1) / BM;
     const long n_tiles = (p.n + NOUT - 1) / NOUT;
     const long grid = (m_blocks * n_tiles + kXcds - 1) / kXcds * kXcds;
     if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
-    mfma_gemm<BM, BN, WM, WN, STAGES, AM, EPI, BK, PD><<<(unsigned)grid, 64 * WM * WN, 0, s>>>(p);
+    mfma_gemm<BM, BN, WM, WN, STAGES, AM, EPI, BK, WL><<<(unsigned)grid, 64 * WM * WN, 0, s>>>(p);
     return (int)hipGetLastError();
 }
 
@@ -924,13 +918,18 @@ int launch_lds(const GemmArgs& p, bool aligned, hipStream_t s) {
 // batch (U) were chosen by measurement on MI355X: SiLU gate_up streams two
 // weight rows per output column and prefers NB=1; single-stream projections
 // prefer NB=4.
-template <int AM, int EPI, int RT>
+template <int AM, int EPI, int RT, int WL>
 int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
-    constexpr int NB = EPI == kEpiSilu ? 1 : 4, U = 4;
+    // Row-major weights: SiLU streams two weight rows per column and prefers
+    // one 16-column block per wave; single-stream projections prefer four.
+    // Frag16 weights (1 KB contiguous fragments): two blocks per wave, with
+    // deeper K batches for the single-stream projections.
+    constexpr int NB = WL == kWeightsFrag16 ? 2 : (EPI == kEpiSilu ? 1 : 4);
+    constexpr int U = WL == kWeightsFrag16 && EPI != kEpiSilu ? 8 : 4;
     const int rows = 16 * RT;
     const long m_blocks = (p.rows + rows - 1) / rows;
     if (!aligned) {
-        if (RT != 1) return kInvalid;
+        if (RT != 1 || WL != kWeightsRowMajor) return kInvalid;
         const long n_blocks = (p.n + 15) / 16;
         const long groups = (m_blocks * n_blocks + kStreamWaves - 1) / kStreamWaves;
         const long grid = (groups + kXcds - 1) / kXcds * kXcds;
@@ -941,7 +940,7 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
     const long groups = (m_blocks * n_blocks + kStreamWaves - 1) / kStreamWaves;
     const long grid = (groups + kXcds - 1) / kXcds * kXcds;
     if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
-    stream_gemm_fast<AM, EPI, NB, U, kStreamWaves, RT><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
+    stream_gemm_fast<AM, EPI, NB, U, kStreamWaves, RT, WL><<<(unsigned)grid, 64 * kStreamWaves, 0, s>>>(p);
     return (int)hipGetLastError();
 }
 
@@ -951,28 +950,47 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
 // MFMA tiles (64x256 with 4 waves, 128x128 with 4 waves, 256x256 with 16
 // waves), measured best on MI355X for the prefill shapes; shapes the MFMA
 // kernel cannot take (K not a multiple of 64, unaligned rows, FP32 output)
-// use the register-staged LDS kernel.
-template <int AM, int EPI>
+// use the register-staged LDS kernel, which reads row-major weights only.
+template <int AM, int EPI, int WL>
 int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
     const bool mfma_ok = aligned && p.k % 64 == 0 && EPI != kEpiStoreF32;
     if constexpr (EPI != kEpiStoreF32) {
         if (mfma_ok) {
             switch (bm) {
-                case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI>(p, s);
-                case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI>(p, s);
-                case 256: return launch_mfma<256, 256, 8, 2, 2, AM, EPI>(p, s);
+                case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(p, s);
+                case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL>(p, s);
+                case 256: return launch_mfma<256, 256, 8, 2, 2, AM, EPI, 64, WL>(p, s);
                 default: break;
             }
         }
     }
     switch (bm) {
-        case 16: return launch_stream<AM, EPI, 1>(p, aligned, s);
-        case 32: return aligned ? launch_stream<AM, EPI, 2>(p, aligned, s) : launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
-        case 64: return launch_lds<64, 128, 2, 2, AM, EPI>(p, aligned, s);
-        case 128: return launch_lds<128, 128, 2, 2, AM, EPI>(p, aligned, s);
-        case 256: return launch_lds<256, 128, 4, 2, AM, EPI>(p, aligned, s);
-        default: return kInvalid;
+        case 16: return launch_stream<AM, EPI, 1, WL>(p, aligned, s);
+        case 32:
+            if (aligned) return launch_stream<AM, EPI, 2, WL>(p, aligned, s);
+            break;
+        default: break;
     }
+    if constexpr (WL != kWeightsRowMajor) {
+        return kInvalid;
+    } else {
+        switch (bm) {
+            case 32: return launch_lds<32, 128, 1, 2, AM, EPI>(p, aligned, s);
+            case 64: return launch_lds<64, 128, 2, 2, AM, EPI>(p, aligned, s);
+            case 128: return launch_lds<128, 128, 2, 2, AM, EPI>(p, aligned, s);
+            case 256: return launch_lds<256, 128, 4, 2, AM, EPI>(p, aligned, s);
+            default: return kInvalid;
+        }
+    }
+}
+
+template <int AM, int EPI>
+int launch_layout(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
+    if (p.w_layout == kWeightsFrag16) {
+        if constexpr (EPI == kEpiStoreF32) return kInvalid;
+        else return launch_by_rows<AM, EPI, kWeightsFrag16>(p, bm, aligned, s);
+    }
+    return launch_by_rows<AM, EPI, kWeightsRowMajor>(p, bm, aligned, s);
 }
 
 }  // namespace
@@ -990,18 +1008,22 @@ int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hip
     if (epilogue == kEpiScatterWeighted && !p.routes) return kInvalid;
     const bool aligned = p.k % 8 == 0 && p.lda % 8 == 0 && ((uintptr_t)p.a % 16) == 0 && ((uintptr_t)p.w % 16) == 0 &&
                          (p.w_expert_stride % 8) == 0;
+    if (p.w_layout == kWeightsFrag16 &&
+        (!aligned || p.k % 64 || p.n % 16 || p.w_up_offset % 16 || epilogue == kEpiStoreF32))
+        return kInvalid;
+    if (p.w_layout != kWeightsRowMajor && p.w_layout != kWeightsFrag16) return kInvalid;
     if (a_mode == kAGather) {
         switch (epilogue) {
-            case kEpiSilu: return launch_by_rows<kAGather, kEpiSilu>(p, bm, aligned, s);
-            case kEpiStoreBf16: return launch_by_rows<kAGather, kEpiStoreBf16>(p, bm, aligned, s);
+            case kEpiSilu: return launch_layout<kAGather, kEpiSilu>(p, bm, aligned, s);
+            case kEpiStoreBf16: return launch_layout<kAGather, kEpiStoreBf16>(p, bm, aligned, s);
             default: return kInvalid;
         }
     }
     switch (epilogue) {
-        case kEpiSilu: return launch_by_rows<kADirect, kEpiSilu>(p, bm, aligned, s);
-        case kEpiStoreBf16: return launch_by_rows<kADirect, kEpiStoreBf16>(p, bm, aligned, s);
-        case kEpiScatterWeighted: return launch_by_rows<kADirect, kEpiScatterWeighted>(p, bm, aligned, s);
-        case kEpiStoreF32: return launch_by_rows<kADirect, kEpiStoreF32>(p, bm, aligned, s);
+        case kEpiSilu: return launch_layout<kADirect, kEpiSilu>(p, bm, aligned, s);
+        case kEpiStoreBf16: return launch_layout<kADirect, kEpiStoreBf16>(p, bm, aligned, s);
+        case kEpiScatterWeighted: return launch_layout<kADirect, kEpiScatterWeighted>(p, bm, aligned, s);
+        case kEpiStoreF32: return launch_layout<kADirect, kEpiStoreF32>(p, bm, aligned, s);
         default: return kInvalid;
     }
 }

@@ -6,6 +6,11 @@ namespace tau_amd {
 
 enum AMode { kAGather = 0, kADirect = 1 };
 enum Epilogue { kEpiSilu = 0, kEpiStoreBf16 = 1, kEpiScatterWeighted = 2, kEpiStoreF32 = 3 };
+// Expert weight layouts.  Row-major: W[e][n][k].  Frag16: each 16-row x 32-wide
+// K block is one contiguous 1 KB MFMA operand fragment, 16-byte piece p holding
+// row 16*nb + p%16, columns 32*kc + 8*(p/16) .. +8; blocks run K-fastest, so a
+// 16-row band of one expert is 16*K contiguous elements.
+enum WeightLayout { kWeightsRowMajor = 0, kWeightsFrag16 = 1 };
 
 struct GemmArgs {
     const uint16_t* a;        // gather: x [T,lda]; direct: rows [rows,lda]
@@ -24,10 +29,12 @@ struct GemmArgs {
     int ldo;                  // output row stride (elements)
     long w_expert_stride;     // elements between experts
     int w_up_offset;          // rows between gate row j and up row j (I)
+    int w_layout;             // WeightLayout of w
     int* receipt;             // optional 5 words stamped by the executed kernel
 };
 
 int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s);
+int launch_pack_frag16(const void* src, void* dst, int experts, int rows, int cols, hipStream_t s);
 bool gemm_rows_supported(int bm);
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);

@@ -39,8 +39,9 @@ bool reference_tile_ok(const TauGemmTile* c) {
 
 GemmArgs gate_up_args(const void* input, const void* gate_up, const float* routes, const int* slots,
                       const int* tiles, const int* meta_total, void* out, int tokens, int top_k, int capacity,
-                      int hidden, int intermediate, int* receipt) {
+                      int hidden, int intermediate, int* receipt, int weight_layout) {
     GemmArgs g{};
+    g.w_layout = weight_layout;
     g.a = (const uint16_t*)input;
     g.w = (const uint16_t*)gate_up;
     g.routes = routes;
@@ -63,8 +64,9 @@ GemmArgs gate_up_args(const void* input, const void* gate_up, const float* route
 
 GemmArgs down_args(const void* activated, const void* down, const float* routes, const int* slots,
                    const int* tiles, const int* meta_total, void* contributions, int tokens, int top_k,
-                   int capacity, int hidden, int intermediate, int* receipt) {
+                   int capacity, int hidden, int intermediate, int* receipt, int weight_layout) {
     GemmArgs g{};
+    g.w_layout = weight_layout;
     g.a = (const uint16_t*)activated;
     g.w = (const uint16_t*)down;
     g.routes = routes;
@@ -91,9 +93,23 @@ bool shape_ok(int tokens, int hidden, int intermediate, int experts, int top_k) 
            (int64_t)tokens * top_k * hidden <= (int64_t)1 << 40;
 }
 
+// Frag16 weights need 16-row bands (gate, up and down rows) and K in whole
+// 64-wide MFMA steps for every projection of the layer.
+bool layout_ok(int weight_layout, int hidden, int intermediate) {
+    if (weight_layout == TAU_MOE_WEIGHTS_ROW_MAJOR) return true;
+    return weight_layout == TAU_MOE_WEIGHTS_FRAG16 && hidden % 64 == 0 && intermediate % 64 == 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int tau_moe_pack_weights(const void* src, void* dst, int experts, int rows, int columns, void* stream) {
+    if (!src || !dst || src == dst || experts <= 0 || rows <= 0 || columns <= 0 || rows % 16 || columns % 64 ||
+        (long)experts * rows * columns / 8 > INT_MAX)
+        return kInvalid;
+    return launch_pack_frag16(src, dst, experts, rows, columns, as_stream(stream));
+}
 
 const char* tau_moe_build_target(void) { return "gfx950"; }
 
@@ -202,9 +218,10 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                               const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                               void* activated, void* contributions, void* output, int tokens, int hidden,
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                              int* receipts, void* stream) {
+                              int weight_layout, int* receipts, void* stream) {
     if (!input || !logits || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
         !contributions || !output || !shape_ok(tokens, hidden, intermediate, experts, top_k) ||
+        !layout_ok(weight_layout, hidden, intermediate) ||
         !gemm_rows_supported(tile_rows) || capacity < capacity_for(tokens, experts, top_k, tile_rows) ||
         capacity % tile_rows)
         return kInvalid;
@@ -216,11 +233,11 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
     if (code) return code;
     const int* total = meta + 2 * experts + 1;
     GemmArgs g = gate_up_args(input, gate_up, routes, slots, tiles, total, activated, tokens, top_k, capacity,
-                              hidden, intermediate, receipts);
+                              hidden, intermediate, receipts, weight_layout);
     code = launch_grouped_gemm(g, tile_rows, kAGather, kEpiSilu, s);
     if (code) return code;
     GemmArgs d = down_args(activated, down, routes, slots, tiles, total, contributions, tokens, top_k, capacity,
-                           hidden, intermediate, receipts ? receipts + 5 : nullptr);
+                           hidden, intermediate, receipts ? receipts + 5 : nullptr, weight_layout);
     code = launch_grouped_gemm(d, tile_rows, kADirect, kEpiScatterWeighted, s);
     if (code) return code;
     return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, s);
@@ -229,20 +246,21 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
 int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* routes, const int* slots,
                                    const int* tiles, const int* meta, void* out, int tokens, int hidden,
                                    int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                                   int projection, int* receipt, void* stream) {
+                                   int projection, int weight_layout, int* receipt, void* stream) {
     if (!a || !w || !routes || !slots || !tiles || !meta || !out ||
         !shape_ok(tokens, hidden, intermediate, experts, top_k) || !gemm_rows_supported(tile_rows) ||
+        !layout_ok(weight_layout, hidden, intermediate) ||
         capacity < capacity_for(tokens, experts, top_k, tile_rows) || capacity % tile_rows ||
         (projection != 0 && projection != 1))
         return kInvalid;
     const int* total = meta + 2 * experts + 1;
     if (projection == 0) {
         GemmArgs g = gate_up_args(a, w, routes, slots, tiles, total, out, tokens, top_k, capacity, hidden,
-                                  intermediate, receipt);
+                                  intermediate, receipt, weight_layout);
         return launch_grouped_gemm(g, tile_rows, kAGather, kEpiSilu, as_stream(stream));
     }
     GemmArgs d = down_args(a, w, routes, slots, tiles, total, out, tokens, top_k, capacity, hidden, intermediate,
-                           receipt);
+                           receipt, weight_layout);
     return launch_grouped_gemm(d, tile_rows, kADirect, kEpiScatterWeighted, as_stream(stream));
 }
 
@@ -257,7 +275,8 @@ int tau_launch_moe_prefill(const void* input, const void* logits, const void* ga
         return kInvalid;
     return tau_launch_moe_prefill_ex(input, logits, 1, gate_up, down, routes, meta, offsets, slots, tiles,
                                      activated, contributions, output, tokens, hidden, intermediate, kRefExperts,
-                                     kRefTopK, gate_up_config->m, capacity, receipts, stream);
+                                     kRefTopK, gate_up_config->m, capacity, TAU_MOE_WEIGHTS_ROW_MAJOR, receipts,
+                                     stream);
 }
 
 int tau_launch_silu_and_mul(const void* input, void* output, int rows, int columns, int dtype, void* stream) {
@@ -290,17 +309,19 @@ int tau_launch_linear_bf16_fp32(const void* input, const void* weight, float* ou
 int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, const void* down_s,
                                     const void* gate_weight, const void* routed, void* activated_ws,
                                     void* shared_ws, void* output, int tokens, int hidden,
-                                    int shared_intermediate, void* stream) {
+                                    int shared_intermediate, int weight_layout, void* stream) {
     if (!input || !gate_up_s || !down_s || !routed || !activated_ws || !shared_ws || !output || tokens <= 0 ||
-        tokens > kMaxTokens || hidden <= 0 || shared_intermediate <= 0)
+        tokens > kMaxTokens || hidden <= 0 || shared_intermediate <= 0 ||
+        !layout_ok(weight_layout, hidden, shared_intermediate))
         return kInvalid;
     hipStream_t s = as_stream(stream);
     const int bm = tokens <= 16 ? 16 : (tokens <= 64 ? 64 : 128);
     GemmArgs g = gate_up_args(input, gate_up_s, nullptr, nullptr, nullptr, nullptr, activated_ws, tokens, 1,
-                              tokens, hidden, shared_intermediate, nullptr);
+                              tokens, hidden, shared_intermediate, nullptr, weight_layout);
     int code = launch_grouped_gemm(g, bm, kADirect, kEpiSilu, s);
     if (code) return code;
     GemmArgs d{};
+    d.w_layout = weight_layout;
     d.a = (const uint16_t*)activated_ws;
     d.w = (const uint16_t*)down_s;
     d.out = shared_ws;

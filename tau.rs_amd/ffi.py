@@ -36,8 +36,13 @@ EXPORTS = (
     "tau_launch_moe_prefill_ex",
     "tau_launch_moe_shared_expert_ex",
     "tau_launch_moe_grouped_gemm_ex",
+    "tau_moe_pack_weights",
     "tau_moe_build_target",
 )
+
+# Expert weight layouts (TAU_MOE_WEIGHTS_* in include/tau_moe.h).
+WEIGHTS_ROW_MAJOR = 0
+WEIGHTS_FRAG16 = 1
 
 
 class TauGemmTile(ctypes.Structure):
@@ -87,9 +92,10 @@ def lib():
         "tau_launch_moe_routing_ex": [p, i, p, i, i, i, p],
         "tau_launch_moe_prefill_dispatch_ex": [p, i, p, p, p, p, p, i, i, i, i, i, p],
         "tau_launch_moe_prefill_combine_ex": [p, p, p, i, i, i, i, p],
-        "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, p, p],
-        "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, p],
-        "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 8 + [p, p],
+        "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p, p],
+        "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, i, p],
+        "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
+        "tau_moe_pack_weights": [p, p, i, i, i, p],
     }
     for name, args in sig.items():
         fn = getattr(L, name)
@@ -159,31 +165,33 @@ def dispatch_ex(logits, routes, meta, offsets, slots, tiles, tokens, experts, to
     check(code, "MoE dispatch")
 
 
-def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, receipts=None, stream=None):
+def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, receipts=None, stream=None,
+               weight_layout=WEIGHTS_ROW_MAJOR):
     t, h = x.shape
     i = down.shape[2]
     code = lib().tau_launch_moe_prefill_ex(
         ptr(x), ptr(logits), _dtype_code(logits), ptr(gate_up), ptr(down), ptr(ws["routes"]), ptr(ws["meta"]),
         ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["activated"]),
         ptr(ws["contributions"]), ptr(output), t, h, i, experts, top_k, tile_rows, ws["capacity"],
-        ptr(receipts), stream_ptr(stream))
+        weight_layout, ptr(receipts), stream_ptr(stream))
     check(code, "MoE grouped prefill")
 
 
-def shared_expert_ex(x, gate_up_s, down_s, gate_weight, routed, activated_ws, shared_ws, output, stream=None):
+def shared_expert_ex(x, gate_up_s, down_s, gate_weight, routed, activated_ws, shared_ws, output, stream=None,
+                     weight_layout=WEIGHTS_ROW_MAJOR):
     t, h = x.shape
     i_s = down_s.shape[1]
     code = lib().tau_launch_moe_shared_expert_ex(
         ptr(x), ptr(gate_up_s), ptr(down_s), ptr(gate_weight), ptr(routed), ptr(activated_ws), ptr(shared_ws),
-        ptr(output), t, h, i_s, stream_ptr(stream))
+        ptr(output), t, h, i_s, weight_layout, stream_ptr(stream))
     check(code, "MoE shared expert")
 
 
 def grouped_gemm_ex(a, w, ws, out, tokens, hidden, intermediate, experts, top_k, tile_rows, projection,
-                    receipt=None, stream=None):
+                    receipt=None, stream=None, weight_layout=WEIGHTS_ROW_MAJOR):
     code = lib().tau_launch_moe_grouped_gemm_ex(
         ptr(a), ptr(w), ptr(ws["routes"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["meta"]), ptr(out), tokens,
-        hidden, intermediate, experts, top_k, tile_rows, ws["capacity"], projection, ptr(receipt),
+        hidden, intermediate, experts, top_k, tile_rows, ws["capacity"], projection, weight_layout, ptr(receipt),
         stream_ptr(stream))
     check(code, "MoE grouped GEMM")
 
@@ -192,3 +200,15 @@ def combine_ex(contributions, output, meta, tokens, hidden, experts, top_k, stre
     code = lib().tau_launch_moe_prefill_combine_ex(ptr(contributions), ptr(output), ptr(meta), tokens, hidden,
                                                    experts, top_k, stream_ptr(stream))
     check(code, "MoE combine")
+
+
+def pack_weights(w: torch.Tensor, stream=None) -> torch.Tensor:
+    """FRAG16 copy of row-major BF16 weights [E, n, k] (or [n, k]); same shape,
+    fragment-ordered contents (TAU_MOE_WEIGHTS_FRAG16)."""
+    if w.dtype != torch.bfloat16 or not w.is_contiguous():
+        raise TypeError("pack_weights expects contiguous BF16 weights")
+    e, n, k = (1, *w.shape) if w.dim() == 2 else w.shape
+    out = torch.empty_like(w)
+    check(lib().tau_moe_pack_weights(ptr(w), ptr(out), e, n, k, stream_ptr(stream)), "MoE weight pack")
+    return out
+

@@ -111,10 +111,15 @@ def _next_pow2(n: int) -> int:
 
 
 class MoePrefillRunner:
-    """Owns the routed-expert weights and the grouped-prefill workspaces."""
+    """Owns the routed-expert weights and the grouped-prefill workspaces.
+
+    weight_layout: "auto" keeps a FRAG16 copy of the weights (1 KB MFMA operand
+    fragments, see include/tau_moe.h) when the shape allows it (hidden and
+    intermediate multiples of 64) and the caller's row-major tensors otherwise;
+    "row_major" / "frag16" force one layout."""
 
     def __init__(self, config: SparseMoeConfig, gate_up: torch.Tensor, down: torch.Tensor,
-                 tile_rows: Optional[int] = None):
+                 tile_rows: Optional[int] = None, weight_layout: str = "auto"):
         config.validate()
         E, I, H = config.num_experts, config.expert_intermediate_size, config.hidden_size
         if gate_up.shape != (E, 2 * I, H) or down.shape != (E, H, I):
@@ -122,8 +127,19 @@ class MoePrefillRunner:
         if gate_up.dtype != torch.bfloat16 or down.dtype != torch.bfloat16 or not gate_up.is_cuda:
             raise ValueError("the HIP path takes contiguous BF16 device weights")
         self.config = config
-        self.gate_up = gate_up.contiguous()
-        self.down = down.contiguous()
+        packable = H % 64 == 0 and I % 64 == 0
+        if weight_layout not in ("auto", "row_major", "frag16"):
+            raise ValueError(f"unknown weight layout {weight_layout!r}")
+        if weight_layout == "frag16" and not packable:
+            raise ValueError("frag16 weights need hidden and intermediate sizes divisible by 64")
+        if weight_layout == "frag16" or (weight_layout == "auto" and packable):
+            self.layout = ffi.WEIGHTS_FRAG16
+            self.gate_up = ffi.pack_weights(gate_up.contiguous())
+            self.down = ffi.pack_weights(down.contiguous())
+        else:
+            self.layout = ffi.WEIGHTS_ROW_MAJOR
+            self.gate_up = gate_up.contiguous()
+            self.down = down.contiguous()
         self.fixed_tile_rows = tile_rows
         self._ws = None
         self._ws_key = None
@@ -187,7 +203,8 @@ class MoePrefillRunner:
         if out is None:
             out = torch.empty_like(x)
         ffi.prefill_ex(x.contiguous(), logits.contiguous(), self.gate_up, self.down, ws, out, c.num_experts,
-                       c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream)
+                       c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream,
+                       weight_layout=self.layout)
         self._calls += 1
         return out
 
@@ -209,8 +226,8 @@ class SparseMoeBlock:
     """Routed experts plus the optional always-on shared expert."""
 
     def __init__(self, config: SparseMoeConfig, gate_up, down, shared_gate_up=None, shared_down=None,
-                 shared_gate=None, tile_rows: Optional[int] = None):
-        self.runner = MoePrefillRunner(config, gate_up, down, tile_rows)
+                 shared_gate=None, tile_rows: Optional[int] = None, weight_layout: str = "auto"):
+        self.runner = MoePrefillRunner(config, gate_up, down, tile_rows, weight_layout)
         self.config = config
         self.shared = None
         if config.shared_expert is not None:
@@ -218,8 +235,13 @@ class SparseMoeBlock:
                 raise ValueError("shared expert weights missing")
             if config.shared_expert.gated and shared_gate is None:
                 raise ValueError("shared expert gate weight missing")
-            self.shared = (shared_gate_up.contiguous(), shared_down.contiguous(),
-                           shared_gate.contiguous() if config.shared_expert.gated else None)
+            gu, dn = shared_gate_up.contiguous(), shared_down.contiguous()
+            Is, H = config.shared_expert.intermediate_size, config.hidden_size
+            self.shared_layout = ffi.WEIGHTS_ROW_MAJOR
+            if self.runner.layout == ffi.WEIGHTS_FRAG16 and Is % 64 == 0 and H % 64 == 0:
+                gu, dn = ffi.pack_weights(gu), ffi.pack_weights(dn)
+                self.shared_layout = ffi.WEIGHTS_FRAG16
+            self.shared = (gu, dn, shared_gate.contiguous() if config.shared_expert.gated else None)
         self._shared_ws = None
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor, stream=None) -> torch.Tensor:
@@ -234,5 +256,6 @@ class SparseMoeBlock:
             self._shared_ws = (torch.empty(n, Is, dtype=torch.bfloat16, device=x.device),
                                torch.empty(n, x.shape[1], dtype=torch.bfloat16, device=x.device))
         act, sh = self._shared_ws
-        ffi.shared_expert_ex(x, gu, dn, gw, routed, act[:T], sh[:T], routed, stream=stream)
+        ffi.shared_expert_ex(x, gu, dn, gw, routed, act[:T], sh[:T], routed, stream=stream,
+                             weight_layout=self.shared_layout)
         return routed

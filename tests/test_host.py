@@ -74,3 +74,39 @@ def test_prefill_tile_parse_and_validate(tau):
     for bad in ["16,64,64,4", "16,64,64,4,1,1", "a,b,c,d,e", "24,64,64,4,1", "16,64,64,3,1"]:
         with pytest.raises(ValueError):
             T.parse(bad)
+
+
+def test_frag16_host_orders_agree_and_match_spot_values():
+    import numpy as np
+    from frag16_host import frag16_loop, frag16_permute
+    rng = np.random.default_rng(5)
+    for shape in [(2, 32, 128), (48, 64), (1, 16, 64)]:
+        w = rng.integers(0, 1 << 16, size=shape, dtype=np.uint16)
+        a, b = frag16_loop(w), frag16_permute(w)
+        np.testing.assert_array_equal(a, b)
+        assert sorted(a.ravel().tolist()) == sorted(w.ravel().tolist())  # a permutation
+    # Spot values fixed by the definition, independent of both restatements:
+    # element (row, col) of a [n, k] matrix at flat index row * k + col.
+    n, k = 32, 128
+    w = np.arange(n * k, dtype=np.int64).reshape(n, k)
+    p = frag16_loop(w).reshape(-1, 8)
+    assert p[0].tolist() == list(range(0, 8))                      # row 0, cols 0..7
+    assert p[1].tolist() == list(range(k, k + 8))                  # lane 1 -> row 1
+    assert p[16].tolist() == list(range(8, 16))                    # lane 16 -> cols 8..15
+    assert p[64].tolist() == list(range(32, 40))                   # next 32-wide K chunk
+    assert p[(k // 32) * 64].tolist() == list(range(16 * k, 16 * k + 8))  # next 16-row band
+
+
+def test_frag16_entry_points_reject_unsupported_shapes(tau):
+    L = tau.ffi.lib()
+    d = ctypes.c_void_p(16)
+    e = ctypes.c_void_p(4096)
+    assert L.tau_moe_pack_weights(d, e, 2, 24, 128, None) == 1   # rows % 16
+    assert L.tau_moe_pack_weights(d, e, 2, 32, 96, None) == 1    # columns % 64
+    assert L.tau_moe_pack_weights(d, d, 2, 32, 128, None) == 1   # in place
+    args = [d] * 13
+    # hidden 96 is not a whole number of 64-wide K steps: frag16 rejected
+    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 96, 128, 8, 2, 16, 4096, 1, None, None) == 1
+    # unknown layout code
+    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 128, 128, 8, 2, 16, 4096, 7, None, None) == 1
+    assert L.tau_launch_moe_grouped_gemm_ex(*([d] * 7), 64, 96, 128, 8, 2, 16, 4096, 0, 1, None, None) == 1
