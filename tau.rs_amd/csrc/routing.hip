@@ -23,8 +23,11 @@
 //    workgroup chunks, and each assignment lands at
 //    offset[e] + earlier-chunk count + earlier-wave count + in-wave rank, which
 //    is the token-ascending order of the reference's CPU plan.  Small batches
-//    run route + plan + scatter in one workgroup; large ones use three
-//    launches (route+histogram per chunk, plan, scatter per chunk).
+//    run route + plan + scatter in one workgroup; large ones route over the
+//    whole GPU, then histogram chunks, then scatter chunks (each chunk
+//    workgroup recomputing the small plan from the chunk counts).
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace tau_amd {
@@ -34,6 +37,7 @@ namespace {
 // Row (16-lane) DPP reductions; every lane of the row receives the result.
 // ---------------------------------------------------------------------------
 constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kRowHalfMirror = 0x141, kRowMirror = 0x140;
+constexpr int kRowShr1 = 0x111;  // lane i reads lane i-1 of its row (lane 0 of the row reads 0)
 
 template <int Ctrl>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
@@ -88,6 +92,11 @@ __device__ __forceinline__ uint32_t orderable(float v) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inverse of orderable().
+__device__ __forceinline__ float from_orderable(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p, size_t i);
 template <>
@@ -109,11 +118,18 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
     float d[EP], p[EP];  // p: exp(x - max) numerators
     uint32_t nonfinite = 0;
     float maximum = -INFINITY;
+    // Unconditional loads (clamped index) so all EP loads are in flight at
+    // once; a guarded load becomes a branch that waits for each in turn.
 #pragma unroll
     for (int j = 0; j < EP; ++j) {
         const int e = j * 16 + l16;
-        d[j] = e < E ? load_logit<T>(row, e) : -INFINITY;
-        if (e < E && !__builtin_isfinite(d[j])) nonfinite = 1;
+        d[j] = load_logit<T>(row, e < E ? e : 0);
+    }
+#pragma unroll
+    for (int j = 0; j < EP; ++j) {
+        const bool in = j * 16 + l16 < E;
+        nonfinite |= (uint32_t)(in && !__builtin_isfinite(d[j]));
+        d[j] = in ? d[j] : -INFINITY;
         maximum = fmaxf(maximum, d[j]);
     }
     nonfinite = row_or(nonfinite);
@@ -128,35 +144,108 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
     }
     const float denominator = row_sum(local);
 
-    uint32_t taken = 0;
     float selected_sum = 0.f;
     int my_id[2] = {0, 0};
     float my_p[2] = {0.f, 0.f};
-    for (int r = 0; r < K; ++r) {
-        uint64_t best = 0;
+    // Rank r's pick is published to lane r % 16 of the row (slot r / 16).
+    auto publish = [&](int r, uint64_t best) {
+        const int id = (int)(0xffffffffu - (uint32_t)best);
+        // Softmax probability exp(x - max) / sum: exp of the very value the key
+        // was made from (orderable() is a bijection), so it equals the
+        // numerator summed above bit for bit.
+        const float prob = expf(from_orderable((uint32_t)(best >> 32))) / denominator;
+        selected_sum += prob;  // rank order, as routing.rs:187-191
+        if (l16 == (r & 15)) {
+            if (r < 16) { my_id[0] = id; my_p[0] = prob; }
+            else { my_id[1] = id; my_p[1] = prob; }
+        }
+    };
+    // pick(): the next expert of the row by (probability desc, id asc), as a
+    // 64-bit key (orderable(x - max), ~id) identical on all 16 lanes.
+    // Up to 16 keys per lane: each lane sorts its keys once (bitonic network,
+    // descending) and a pick is the row max of the lane heads; its owner
+    // advances.  32 keys per lane: a strict '>' scan over the untaken 32-bit
+    // values in slot order (the smallest id wins a tie within the lane).
+    uint64_t key[EP <= 16 ? EP : 1];
+    uint32_t ord[EP <= 16 ? 1 : EP];
+    int h = 0;           // sorted form: keys this lane has given up
+    uint32_t taken = 0;  // scan form: slots already picked
+    if constexpr (EP <= 16) {
 #pragma unroll
         for (int j = 0; j < EP; ++j) {
             const int e = j * 16 + l16;
-            if (e < E && !(taken & (1u << j))) {
-                const uint64_t key = ((uint64_t)orderable(d[j]) << 32) | (0xffffffffu - (uint32_t)e);
-                best = key > best ? key : best;
-            }
+            key[j] = e < E ? ((uint64_t)orderable(d[j]) << 32) | (0xffffffffu - (uint32_t)e) : 0;
         }
-        best = row_max_u64(best);
-        const int id = (int)(0xffffffffu - (uint32_t)best);
-        const int owner = id & 15, slot = id >> 4;
-        float mine = 0.f;
 #pragma unroll
-        for (int j = 0; j < EP; ++j)
-            if (j == slot && l16 == owner) mine = p[j];
-        // Softmax probability of the selected expert, exp(x - max) / sum.
-        const float prob = row_sum(mine) / denominator;  // one non-zero term: exact sum
-        if (l16 == owner) taken |= 1u << slot;
-        selected_sum += prob;  // rank order, as routing.rs:187-191
-        if (l16 == (r & 15)) {
-            my_id[r >> 4] = id;
-            my_p[r >> 4] = prob;
+        for (int size = 2; size <= EP; size <<= 1)
+#pragma unroll
+            for (int stride = size / 2; stride > 0; stride >>= 1)
+#pragma unroll
+                for (int i = 0; i < EP; ++i) {
+                    const int j = i ^ stride;
+                    if (j > i) {
+                        const uint64_t a = key[i], b = key[j];
+                        const bool swap = (i & size) == 0 ? a < b : a > b;
+                        key[i] = swap ? b : a;
+                        key[j] = swap ? a : b;
+                    }
+                }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EP; ++j) ord[j] = j * 16 + l16 < E ? orderable(d[j]) : 0u;  // valid values are > 0
+    }
+    auto pick = [&]() -> uint64_t {
+        if constexpr (EP <= 16) {
+            // head = key[h] through a log2(EP)-level select tree; 0 once exhausted
+            uint64_t t[EP];
+#pragma unroll
+            for (int i = 0; i < EP; ++i) t[i] = key[i];
+#pragma unroll
+            for (int w = EP / 2, b = 0; w >= 1; w /= 2, ++b)
+#pragma unroll
+                for (int i = 0; i < w; ++i) t[i] = ((h >> b) & 1) ? t[2 * i + 1] : t[2 * i];
+            const uint64_t mine = h < EP ? t[0] : 0;
+            const uint64_t best = row_max_u64(mine);
+            h += mine == best;  // keys are distinct (ids differ): only the owner advances
+            return best;
+        } else {
+            uint32_t bo = 0;
+            int bj = 0;
+#pragma unroll
+            for (int j = 0; j < EP; ++j) {
+                const uint32_t v = (taken >> j) & 1u ? 0u : ord[j];
+                bj = v > bo ? j : bj;
+                bo = v > bo ? v : bo;
+            }
+            const uint64_t mine = bo ? ((uint64_t)bo << 32) | (0xffffffffu - (uint32_t)(bj * 16 + l16)) : 0;
+            const uint64_t best = row_max_u64(mine);
+            taken |= (mine == best) ? 1u << bj : 0u;
+            return best;
         }
+    };
+    if (K <= 16) {
+        // Picks only record the winning key in lane r; probabilities are then
+        // computed by all ranks at once and summed in rank order.
+        uint64_t picked = 0;
+        for (int r = 0; r < K; ++r) {
+            const uint64_t best = pick();
+            picked = l16 == r ? best : picked;
+        }
+        const bool ranked = l16 < K;
+        const float prob = ranked ? expf(from_orderable((uint32_t)(picked >> 32))) / denominator : 0.f;
+        // Left fold p0 + p1 + ... + p(K-1), as the sequential loop of
+        // routing.rs:187-191: lane r adds its p to lane r-1's partial.
+        float partial = prob;
+        for (int r = 1; r < K; ++r) {
+            const float prev = __uint_as_float(
+                (uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(partial), kRowShr1, 0xf, 0xf, false));
+            partial = l16 == r ? prev + prob : partial;
+        }
+        selected_sum = __shfl(partial, (int)(threadIdx.x & ~15u) + K - 1, 64);
+        my_id[0] = ranked ? (int)(0xffffffffu - (uint32_t)picked) : 0;
+        my_p[0] = prob;
+    } else {
+        for (int r = 0; r < K; ++r) publish(r, pick());
     }
     if (active) {
         float* out = routes + (size_t)t * 2 * K;
@@ -173,9 +262,11 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
     return nonfinite != 0;
 }
 
+// One wavefront (four tokens) per workgroup, so small batches still spread
+// over every CU.
 template <int EP, typename T>
-__global__ __launch_bounds__(256) void route_kernel(const T* logits, float* routes, int T_, int E, int K) {
-    const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
+__global__ __launch_bounds__(64) void route_kernel(const T* logits, float* routes, int T_, int E, int K) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
     route_row<EP, T>(logits, t, t < T_, routes, E, K, nullptr);
 }
 
@@ -185,7 +276,7 @@ __global__ __launch_bounds__(256) void route_kernel(const T* logits, float* rout
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSpanLds = 4096;      // assignments whose experts fit the LDS stage
-constexpr int kPlanLdsWords = 4096; // [chunks][E] counts staged by the plan workgroup
+constexpr int kPlanLdsWords = 4096; // bound on [chunks][E] counts each chunk workgroup sums
 
 // Validates one externally supplied assignment (moe_dispatch.cu:23-33 of the
 // reference): a finite integral id in [0,E), no duplicate among the token's
@@ -194,9 +285,16 @@ __device__ __forceinline__ int assignment_expert(const float* routes, int a, int
     const int t = a / K, r = a - t * K;
     const float* row = routes + (size_t)t * 2 * K;
     const float id = row[r], w = row[K + r];
-    bool valid = __builtin_isfinite(id) && id >= 0.f && id < (float)E && floorf(id) == id &&
-                 __builtin_isfinite(w) && w >= 0.f;
-    for (int q = 0; q < r; ++q) valid &= row[q] != id;  // independent loads, issued together
+    bool dup = false;
+    for (int q0 = 0; q0 < r; q0 += 8) {  // earlier ranks, 8 loads in flight per batch
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = row[min(q0 + u, r)];  // clamped: unconditional loads
+#pragma unroll
+        for (int u = 0; u < 8; ++u) dup |= q0 + u < r && v[u] == id;
+    }
+    const bool valid = __builtin_isfinite(id) && id >= 0.f && id < (float)E && floorf(id) == id &&
+                       __builtin_isfinite(w) && w >= 0.f && !dup;
     return valid ? (int)id : -1;
 }
 
@@ -233,10 +331,11 @@ struct DispatchLds {
     int* flag;      // [1]
     int* scan_tmp;  // [kThreads]
     int* eids;      // [kSpanLds] expert of each assignment of the span
+    int* base;      // [E] multi-workgroup: this chunk's first slot per expert
 };
 
 __host__ __device__ inline size_t dispatch_lds_words(int E) {
-    return (size_t)kWaves * E + E + E + 1 + 1 + kThreads + kSpanLds;
+    return (size_t)kWaves * E + E + E + 1 + 1 + kThreads + kSpanLds + E;
 }
 
 __device__ __forceinline__ DispatchLds dispatch_lds(int* lds, int E) {
@@ -247,6 +346,7 @@ __device__ __forceinline__ DispatchLds dispatch_lds(int* lds, int E) {
     l.flag = l.padded + E + 1;
     l.scan_tmp = l.flag + 1;
     l.eids = l.scan_tmp + kThreads;
+    l.base = l.eids + kSpanLds;
     return l;
 }
 
@@ -327,61 +427,78 @@ __device__ void span_scatter(const DispatchArgs& p, const DispatchLds& l, int be
     }
 }
 
-// Padded exclusive scan of total[] over experts into padded[0..E].
+// Padded exclusive scan of total[] over experts into padded[0..E] (E <=
+// kThreads: one expert per thread): shuffle scan within each wave, wave totals
+// through LDS, one barrier.
 __device__ void padded_scan(const DispatchArgs& p, const DispatchLds& l) {
-    const int tid = threadIdx.x;
-    const int per = (p.E + kThreads - 1) / kThreads;
-    const int e0 = tid * per;
-    int local = 0;
-    for (int e = e0; e < min(p.E, e0 + per); ++e) local += (l.total[e] + p.M - 1) / p.M * p.M;
-    l.scan_tmp[tid] = local;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int v = tid < p.E ? (l.total[tid] + p.M - 1) / p.M * p.M : 0;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) l.scan_tmp[wave] = x;
     __syncthreads();
-    for (int d = 1; d < kThreads; d <<= 1) {
-        const int v = tid >= d ? l.scan_tmp[tid - d] : 0;
-        __syncthreads();
-        l.scan_tmp[tid] += v;
-        __syncthreads();
-    }
-    int run = l.scan_tmp[tid] - local;
-    for (int e = e0; e < min(p.E, e0 + per); ++e) {
-        l.padded[e] = run;
-        run += (l.total[e] + p.M - 1) / p.M * p.M;
-    }
-    if (tid == kThreads - 1) l.padded[p.E] = l.scan_tmp[tid];
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += l.scan_tmp[w];
+    const int exclusive = before + x - v;
+    if (tid < p.E) l.padded[tid] = exclusive;
+    if (tid == p.E - 1) l.padded[p.E] = exclusive + v;
     __syncthreads();
 }
 
-// Metadata words, offsets, the tile worklist and padding sentinels.
-__device__ void finalize_plan(const DispatchArgs& p, const DispatchLds& l, int status) {
+// Metadata words, offsets, the tile worklist and padding sentinels, from the
+// plan in LDS (total = per-expert counts, padded = padded offsets).  Work is
+// split over `parts` workgroups (the chunk workgroups of the multi-workgroup
+// plan); part 0 writes the metadata words.
+__device__ void finalize_part(const DispatchArgs& p, const DispatchLds& l, int status, int part, int parts) {
     const int tid = threadIdx.x;
     const int A = p.tokens * p.K;
     const int padded_total = l.padded[p.E];
-    for (int e = tid; e < p.E; e += kThreads) {
-        p.meta[e] = l.total[e];
-        p.meta[p.E + e] = l.total[e];
-        p.offsets[e] = l.padded[e];
-    }
-    if (tid == 0) {
-        p.offsets[p.E] = padded_total;
-        p.meta[2 * p.E] = status;
-        p.meta[2 * p.E + 1] = padded_total;
-    }
-    const int ntiles = p.capacity / p.M;
-    for (int tile = tid; tile < ntiles; tile += kThreads) {
-        const int row0 = tile * p.M;
-        int e = -1;
-        if (row0 < padded_total) {
-            int lo = 0, hi = p.E - 1;  // last expert with padded[e] <= row0
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (l.padded[mid] <= row0) lo = mid; else hi = mid - 1;
-            }
-            e = lo;
+    if (part == 0) {
+        for (int e = tid; e < p.E; e += kThreads) {
+            p.meta[e] = l.total[e];
+            p.meta[p.E + e] = l.total[e];
+            p.offsets[e] = l.padded[e];
         }
-        p.tiles[tile] = e;
-        const int valid_end = e >= 0 ? l.padded[e] + l.total[e] : 0;
-        for (int row = max(row0, valid_end); row < row0 + p.M; ++row) p.slots[row] = A;
+        if (tid == 0) {
+            p.offsets[p.E] = padded_total;
+            p.meta[2 * p.E] = status;
+            p.meta[2 * p.E + 1] = padded_total;
+        }
     }
+    // Tile worklist and padding sentinels straight from each expert's padded
+    // range [padded[e], padded[e+1]).  This part's experts are e = part +
+    // parts * j; wave w takes j = w, w + 16, ...: lane i first reads expert
+    // j = w + 16 i's range from LDS (one read per lane), then the wave walks
+    // its experts with readlane, its lanes storing 64 consecutive rows
+    // (coalesced) per instruction.
+    const int ntiles = p.capacity / p.M;
+    {
+        const int wave = tid >> 6, lane = tid & 63;
+        const int nmine = part < p.E ? (p.E - part + parts - 1) / parts : 0;
+        const int jl = wave + kWaves * lane;
+        int pb = 0, pe = 0, pt = 0;
+        if (jl < nmine) {
+            const int e = part + parts * jl;
+            pb = l.padded[e];
+            pe = l.padded[e + 1];
+            pt = l.total[e];
+        }
+        const int count = wave < nmine ? (nmine - wave + kWaves - 1) / kWaves : 0;
+        for (int i = 0; i < count; ++i) {
+            const int e = part + parts * (wave + kWaves * i);
+            const int b = __builtin_amdgcn_readlane(pb, i), end = __builtin_amdgcn_readlane(pe, i);
+            const int valid_end = b + __builtin_amdgcn_readlane(pt, i);
+            for (int t = b / p.M + lane; t < end / p.M; t += 64) p.tiles[t] = e;
+            for (int row = valid_end + lane; row < end; row += 64) p.slots[row] = A;
+        }
+    }
+    const int stride = parts * kThreads, first = part * kThreads + tid;
+    for (int t = padded_total / p.M + first; t < ntiles; t += stride) p.tiles[t] = -1;
+    for (long row = (long)padded_total + first; row < p.capacity; row += stride) p.slots[row] = A;
 }
 
 // Routes tokens [t0, t1) with the workgroup (4 tokens per wave per pass),
@@ -426,7 +543,7 @@ __global__ __launch_bounds__(kThreads) void dispatch_single_kernel(DispatchArgs 
     const int status = l.flag[0];
     padded_scan(p, l);
     span_scatter(p, l, 0, A, src, l.padded);
-    finalize_plan(p, l, status);
+    finalize_part(p, l, status, 0, 1);
 }
 
 // Multi-workgroup plan, step 1: route (or stage) one chunk of tokens and
@@ -446,57 +563,57 @@ __global__ __launch_bounds__(kThreads) void dispatch_hist_kernel(DispatchArgs p)
     if (threadIdx.x == 0) p.scratch[(size_t)gridDim.x * p.E + c] = l.flag[0];
 }
 
-// Step 2 (one workgroup): chunk bases per expert, padded offsets, metadata.
-__global__ __launch_bounds__(kThreads) void dispatch_plan_kernel(DispatchArgs p, int chunks) {
-    extern __shared__ int lds[];
-    const DispatchLds l = dispatch_lds(lds, p.E);
-    int* cnt = l.eids;  // [chunks][E] <= kPlanLdsWords <= kSpanLds
-    const int n = chunks * p.E;
-    for (int i = threadIdx.x; i < n; i += kThreads) cnt[i] = p.scratch[i];
-    if (threadIdx.x == 0) l.flag[0] = 0;
-    __syncthreads();
-    for (int c = threadIdx.x; c < chunks; c += kThreads)
-        if (p.scratch[(size_t)chunks * p.E + c]) l.flag[0] = 1;
-    for (int e = threadIdx.x; e < p.E; e += kThreads) {
-        int run = 0;
-        for (int c = 0; c < chunks; ++c) {
-            const int v = cnt[c * p.E + e];
-            cnt[c * p.E + e] = run;
-            run += v;
-        }
-        l.total[e] = run;
-    }
-    __syncthreads();
-    const int status = l.flag[0];
-    padded_scan(p, l);
-    for (int i = threadIdx.x; i < n; i += kThreads) p.scratch[i] = cnt[i] + l.padded[i % p.E];
-    finalize_plan(p, l, status);
-}
-
-// Step 3: stable scatter of each chunk from its absolute per-expert bases.
+// Step 2: every chunk workgroup recomputes the plan from the chunk counts
+// (per-expert totals, its own chunk's prefix, the padded scan; a few KB from
+// L2), writes its share of the tile worklist and sentinels, then scatters its
+// chunk stably from the absolute per-expert bases.
 __global__ __launch_bounds__(kThreads) void dispatch_scatter_kernel(DispatchArgs p) {
     extern __shared__ int lds[];
     const DispatchLds l = dispatch_lds(lds, p.E);
-    const int c = blockIdx.x;
-    const int b = c * p.chunk_tokens * p.K, e_ = min(p.tokens, (c + 1) * p.chunk_tokens) * p.K;
+    const int c = blockIdx.x, chunks = gridDim.x;
     clear_counts(p, l);
+    for (int e = threadIdx.x; e < p.E; e += kThreads) {
+        int run = 0, before = 0;
+        for (int q0 = 0; q0 < chunks; q0 += 8) {  // 8 independent loads in flight per batch
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p.scratch[(size_t)min(q0 + u, chunks - 1) * p.E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int q = q0 + u;
+                before = q == c ? run : before;
+                run += q < chunks ? v[u] : 0;
+            }
+        }
+        l.total[e] = run;
+        l.base[e] = before;
+    }
+    for (int q = threadIdx.x; q < chunks; q += kThreads)
+        if (p.scratch[(size_t)chunks * p.E + q]) l.flag[0] = 1;
+    __syncthreads();
+    const int status = l.flag[0];
+    padded_scan(p, l);
+    for (int e = threadIdx.x; e < p.E; e += kThreads) l.base[e] += l.padded[e];
+    finalize_part(p, l, status, c, chunks);
+    __syncthreads();
+    const int b = c * p.chunk_tokens * p.K, e_ = min(p.tokens, (c + 1) * p.chunk_tokens) * p.K;
     stage_span(p, l, b, e_);  // routes were validated by the histogram step
     __syncthreads();
     const SpanExperts src{l.eids, b};
     span_counts(p, l, b, e_, src, false);
-    span_scatter(p, l, b, e_, src, p.scratch + (size_t)c * p.E);
+    span_scatter(p, l, b, e_, src, l.base);
 }
 
 template <typename T>
 int launch_route(const T* logits, float* routes, int tokens, int E, int K, hipStream_t s) {
-    const int blocks = (tokens + 15) / 16;
+    const int blocks = (tokens + 3) / 4;
     const int ep = (E + 15) / 16;
-    if (ep <= 1) route_kernel<1, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 2) route_kernel<2, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 4) route_kernel<4, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 8) route_kernel<8, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 16) route_kernel<16, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
-    else route_kernel<32, T><<<blocks, 256, 0, s>>>(logits, routes, tokens, E, K);
+    if (ep <= 1) route_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 2) route_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 4) route_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 8) route_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 16) route_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else route_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
     return (int)hipGetLastError();
 }
 
@@ -530,7 +647,7 @@ struct HistLaunch {
 }  // namespace
 
 // Largest expert count the routing/dispatch kernels accept (32 logits per
-// lane of a 16-lane row; dispatch LDS (18 E + 5122) words, 57 KB at E = 512).
+// lane of a 16-lane row; dispatch LDS (19 E + 5122) words, 59 KB at E = 512).
 constexpr int kMaxExperts = 512;
 constexpr int kMaxTopK = 32;
 
@@ -578,8 +695,17 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
     while ((1 << bits) < E) ++bits;
     a.expert_bits = bits;
     const size_t lds = sizeof(int) * dispatch_lds_words(E);
-    a.chunk_tokens = kSpanLds / K / 64 * 64;  // whole 64-token routing passes per chunk
-    if (a.chunk_tokens == 0) a.chunk_tokens = kSpanLds / K;
+    // Multi-workgroup chunks: as many as the plan workgroup can stage
+    // ([chunks][E] counts in LDS, at most 64), each a whole number of 64-token
+    // routing passes that fits the LDS expert stage.
+    {
+        const int max_chunks = std::max(1, std::min(64, kPlanLdsWords / E));
+        const int stage_tokens = std::max(1, kSpanLds / K);
+        int ct = (tokens + max_chunks - 1) / max_chunks;
+        ct = (ct + 63) / 64 * 64;
+        if (ct > stage_tokens) ct = stage_tokens >= 64 ? stage_tokens / 64 * 64 : stage_tokens;
+        a.chunk_tokens = ct;
+    }
     const int chunks = (tokens + a.chunk_tokens - 1) / a.chunk_tokens;
     const bool multi = chunks > 1 && scratch && (size_t)chunks * E <= (size_t)kPlanLdsWords &&
                        scratch_bytes >= sizeof(int) * ((size_t)chunks * E + chunks);
@@ -599,7 +725,6 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
     }
     int code = by_ep<HistLaunch>(E, a, chunks, lds, s);
     if (code) return code;
-    dispatch_plan_kernel<<<1, kThreads, lds, s>>>(a, chunks);
     dispatch_scatter_kernel<<<chunks, kThreads, lds, s>>>(a);
     return (int)hipGetLastError();
 }

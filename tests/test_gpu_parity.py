@@ -140,3 +140,41 @@ def test_full_size_layer_sampled_tokens(tau, oracle, name):
     e = rel_l2(to_np(out)[sel], ref[sel])
     say(f"    rel_l2 vs f32 (96 tokens) {e:.2e}")
     assert e <= 1e-2
+
+
+WIDE = [(64, 32, "bf16"), (512, 20, "bf16"), (512, 32, "f32"), (200, 16, "bf16"), (200, 12, "f32"), (48, 17, "f32")]
+
+
+@pytest.mark.parametrize("case", range(len(WIDE)))
+def test_routing_wide_top_k_with_ties(tau, oracle, case):
+    """K above 16 (ranks published one by one), 13-32 logits per lane (sorted
+    heads and the 32-key scan), coarse logits so that ties are common; both
+    the standalone routing kernel and the routing folded into dispatch."""
+    E, K, dt = WIDE[case]
+    T = 37
+    say(f"[wide routing] E={E} K={K} {dt} T={T}")
+    g = torch.Generator(device="cuda").manual_seed(100 + case)
+    logits = (torch.randint(-6, 7, (T, E), generator=g, device="cuda").float() * 0.25)
+    logits = logits.to(torch.bfloat16) if dt == "bf16" else logits
+    ids_ref, w_ref = oracle.route(to_np(logits), K)
+    routes = torch.empty(T, 2 * K, dtype=torch.float32, device="cuda")
+    tau.ffi.routing_ex(logits, routes, E, K)
+    torch.cuda.synchronize()
+    r = to_np(routes)
+    np.testing.assert_array_equal(r[:, :K].astype(np.int64), ids_ref)
+    assert np.all(np.abs(r[:, K:] - w_ref) <= 1e-7 + 1e-5 * np.abs(w_ref))
+    # routing inside the single-workgroup dispatch
+    M = 16
+    cap = tau.ffi.capacity(T, E, K, M)
+    meta = torch.empty(2 * E + 2, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    slots = torch.empty(cap, dtype=torch.int32, device="cuda")
+    tiles = torch.empty(cap // M, dtype=torch.int32, device="cuda")
+    routes2 = torch.empty_like(routes)
+    tau.ffi.dispatch_ex(logits, routes2, meta, offsets, slots, tiles, T, E, K, M, cap)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_np(routes2), r)
+    m_ref, o_ref, s_ref, t_ref = oracle.dispatch(ids_ref, E, M, cap)
+    np.testing.assert_array_equal(meta.cpu().numpy(), m_ref)
+    np.testing.assert_array_equal(slots.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(tiles.cpu().numpy(), t_ref)
