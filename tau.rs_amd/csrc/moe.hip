@@ -226,6 +226,10 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
         capacity % tile_rows)
         return kInvalid;
     hipStream_t s = as_stream(stream);
+    if (decode_path_supported(tokens, hidden, intermediate, experts, top_k, tile_rows, weight_layout))
+        return launch_decode_moe(input, logits, logits_dtype, gate_up, down, routes, meta, offsets, slots, tiles,
+                                 activated, contributions, output, tokens, hidden, intermediate, experts, top_k,
+                                 capacity, weight_layout, receipts, s);
     // The contributions buffer is free until the down projection: it holds the
     // multi-workgroup dispatch's per-chunk counts.
     int code = launch_dispatch(logits, logits_dtype, routes, meta, offsets, slots, tiles, tokens, experts, top_k,
