@@ -297,13 +297,14 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
     d.w_up_offset = 0;
     d.receipt = receipts ? receipts + 5 : nullptr;
 
-    // Column blocks and K batches as the general path's streaming kernels
-    // (measured on MI355X); the plan workgroup of the down launch has the
-    // same 256 threads as the GEMM workgroups.
+    // Column blocks per wave and K batch depth measured on MI355X for these
+    // kernels (frag16 gate_up 2 x 16 columns, 4 x 32 K; down 4 x 16 columns,
+    // 4 x 32 K); the plan workgroup of the down launch has the same 256
+    // threads as the GEMM workgroups.
     if (weight_layout == kWeightsFrag16) {
         code = launch_decode_gemm<kEpiSilu, 2, 4, 4, kWeightsFrag16, false>(g, plan, 0, s);
         if (code) return code;
-        code = launch_decode_gemm<kEpiScatterWeighted, 2, 8, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
+        code = launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
     } else {
         code = launch_decode_gemm<kEpiSilu, 1, 4, 4, kWeightsRowMajor, false>(g, plan, 0, s);
         if (code) return code;
