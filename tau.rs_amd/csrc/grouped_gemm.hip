@@ -713,6 +713,17 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         wave_rows_live = __any(any);
     }
 
+    // A copies of 8-row groups that are all padding are skipped (padding rows
+    // are a suffix of the tile, so the group's first row decides); their LDS
+    // rows keep stale values, feed only padding rows of the product and are
+    // replaced by zeros in the epilogue.  Safe with two stages, whose wait
+    // drains every outstanding copy whatever their number.
+    bool a_live[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+        const int r = (i * (NT / 64) + wave) * RPI;
+        a_live[i] = STAGES != 2 || !(AM == kAGather || EPI == kEpiScatterWeighted) || row_src[r] >= 0;
+    }
     // Per-lane load sources.  Instruction i of wave w fills rows
     // [q*RPI, (q+1)*RPI) with q = i*(NT/64) + w; lane l supplies row
     // q*RPI + l/CPR into chunk slot l%CPR, i.e. global chunk slot ^ swz(row).
@@ -763,7 +774,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         uint16_t* Bs = As + BM * BK;
         const int kb = kt * BK;
 #pragma unroll
-        for (int i = 0; i < ACH; ++i) lds_dma16(a_src[i] + kb, As + (i * (NT / 64) + wave) * 512);
+        for (int i = 0; i < ACH; ++i)
+            if (a_live[i]) lds_dma16(a_src[i] + kb, As + (i * (NT / 64) + wave) * 512);
 #pragma unroll
         for (int i = 0; i < BCH; ++i)
             lds_dma16(b_src[i] + (WL == kWeightsFrag16 ? kb * 16 : kb), Bs + (i * (NT / 64) + wave) * 512);
@@ -872,20 +884,22 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         const int row = row0 + r;
         if (row >= p.rows) continue;
         long dst;
+        bool pad = false;  // gathered padding row: zero, as the reference's zero-filled A makes it
         if constexpr (EPI == kEpiScatterWeighted) {
             dst = row_src[r];
             if (dst < 0) continue;
         } else {
             dst = row;
+            if constexpr (AM == kAGather) pad = row_src[r] < 0;
         }
         const int col = c0 + sg * 8;
         if (col >= p.n) continue;
         const uint16_t* src = C + r * CSTRIDE + sg * 8;
         uint16_t* o = out + dst * (long)p.ldo + col;
         if (vec && col + 8 <= p.n) {
-            *(u32x4*)o = *(const u32x4*)src;
+            *(u32x4*)o = pad ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)src;
         } else {
-            for (int e = 0; e < 8 && col + e < p.n; ++e) o[e] = src[e];
+            for (int e = 0; e < 8 && col + e < p.n; ++e) o[e] = pad ? (uint16_t)0 : src[e];
         }
     }
 }

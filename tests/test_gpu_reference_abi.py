@@ -201,17 +201,21 @@ def test_reference_grouped_prefill_parity(tau, oracle, h, i):
             assert runner.executed_tiles()[0][0] == m
 
 
-def test_gate_up_projection_is_exact_on_dyadic_operands(tau, oracle):
+@pytest.mark.parametrize("h,i", [(144, 80), (256, 64)])
+def test_gate_up_projection_is_exact_on_dyadic_operands(tau, oracle, h, i):
     """Reference gate_up GEMM (moe_gemm.cu, down == 0) on the reference's dyadic
     generator: every product and partial sum is exact in f32, so the BF16
-    projection must equal the oracle bit for bit at any summation order."""
-    h, i, tokens = 144, 80, 33
+    projection must equal the oracle bit for bit at any summation order, and
+    padding rows (sentinel slots) are zero as the reference's zero-filled A
+    operand makes them.  h = 256 runs the MFMA kernel for 64/128/256-row
+    blocks, h = 144 the register-staged one."""
+    tokens = 33
     L = tau.ffi.lib()
     x, logits, gate_up, down = reference_generator_layer(tokens, h, i)
     xb, gu = bf16(x), bf16(gate_up)
     ids, _ = oracle.route(f32(bf16(logits)), K)
     for m in (16, 32, 64, 128, 256):
-        say(f"[gate_up exact] M={m}")
+        say(f"[gate_up exact] h={h} i={i} M={m}")
         meta, off, slots, tiles = oracle.dispatch(ids, E, m)
         cap = len(slots)
         routes = np.concatenate([ids.astype(np.float32), np.full((tokens, 8), 0.125, np.float32)], axis=1)
