@@ -13,7 +13,8 @@ import os
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtau_moe_hip.so")
+# TAU_MOE_LIBRARY overrides the library file (e.g. an alternative build).
+LIB_PATH = os.environ.get("TAU_MOE_LIBRARY") or os.path.join(HERE, "libtau_moe_hip.so")
 
 # Every symbol declared in include/tau_moe.h.
 EXPORTS = (
