@@ -77,6 +77,16 @@ class Layer:
         self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"], tile_rows=tile_rows or None,
                                            weight_layout=weight_layout)
         self.layout = self.runner.layout
+        self.shared = None
+        if shape.shared_intermediate:  # the always-on shared expert, gated by sigmoid(x . w_s)
+            gu_s, dn_s = self.data["shared_gate_up"], self.data["shared_down"]
+            lay = tau.ffi.WEIGHTS_ROW_MAJOR
+            if self.layout == tau.ffi.WEIGHTS_FRAG16 and shape.shared_intermediate % 64 == 0:
+                gu_s, dn_s, lay = tau.ffi.pack_weights(gu_s), tau.ffi.pack_weights(dn_s), tau.ffi.WEIGHTS_FRAG16
+            T = shape.tokens
+            self.shared = (gu_s, dn_s, self.data["shared_gate"], lay,
+                           torch.empty(T, shape.shared_intermediate, dtype=torch.bfloat16, device="cuda"),
+                           torch.empty(T, shape.hidden, dtype=torch.bfloat16, device="cuda"))
         self.banks = [(self.runner.gate_up, self.runner.down)]
         for _ in range(banks - 1):
             self.banks.append((self.runner.gate_up.clone(), self.runner.down.clone()))
@@ -90,6 +100,10 @@ class Layer:
         s = self.shape
         self.tau.ffi.prefill_ex(self.data["x"], self.data["logits"], gu, dn, self.ws, self.out, s.experts,
                                 s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout)
+        if self.shared is not None:
+            gu_s, dn_s, gate, lay, act, sh = self.shared
+            self.tau.ffi.shared_expert_ex(self.data["x"], gu_s, dn_s, gate, self.out, act, sh, self.out,
+                                          weight_layout=lay)
 
     def projection(self, i, which):
         gu, dn = self.banks[i % len(self.banks)]
@@ -128,6 +142,9 @@ def cpu_baseline(layer, seconds):
     lg = f(layer.data["logits"][:sample])
     gu = f(layer.data["gate_up"])
     dn = f(layer.data["down"])
+    shared = None
+    if s.shared_intermediate:
+        shared = (f(layer.data["shared_gate_up"]), f(layer.data["shared_down"]), f(layer.data["shared_gate"]))
     threads = min(16, os.cpu_count() or 1)
     oracle.set_threads(threads)
     times = []
@@ -135,7 +152,9 @@ def cpu_baseline(layer, seconds):
     while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 25):
         t0 = time.perf_counter()
         ids, w = oracle.route(lg, s.top_k)
-        oracle.moe(x, ids, w, gu, dn)
+        routed = oracle.moe(x, ids, w, gu, dn)
+        if shared is not None:
+            oracle.shared_combine_f32(x, shared[2], oracle.dense_mlp(x, shared[0], shared[1]), routed)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times[1:]) if len(times) > 1 else times[0]
     return {
