@@ -185,6 +185,13 @@ int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, co
                                     void* shared_ws, void* output, int tokens, int hidden,
                                     int shared_intermediate, int weight_layout, void* stream);
 
+/* Router projection (routing.rs:91-93, Router::logits; bias of config.rs:37-78):
+ * logits f32 [T, E] = input BF16 [T, H] . weight BF16 [E, H]^T (+ bias f32 [E],
+ * may be NULL), f32 accumulation, the bias added once after the projection.
+ * Feeds the *_ex entry points with logits_dtype 0. */
+int tau_launch_moe_router_ex(const void* input, const void* weight, const float* bias, float* logits, int tokens,
+                             int hidden, int experts, void* stream);
+
 /* Load-time weight preparation (no reference counterpart: the reference's
  * kernels read its packed [E, n, k] storage directly, sparse_moe/experts.rs:
  * 50-90).  Writes the FRAG16 form of row-major src [experts, rows, columns]

@@ -79,7 +79,22 @@ __global__ void pack_frag16_kernel(const uint16_t* __restrict__ src, uint16_t* _
     }
 }
 
+// out[r, c] += bias[c] (f32, one add after the projection, as a Linear with bias).
+__global__ void add_bias_kernel(float* __restrict__ out, const float* __restrict__ bias, long rows, int cols) {
+    const long n = rows * cols;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+        out[i] += bias[i % cols];
+}
+
 }  // namespace
+
+int launch_add_bias(float* out, const float* bias, int rows, int cols, hipStream_t s) {
+    if (!out || !bias || rows <= 0 || cols <= 0) return kInvalid;
+    long blocks = ((long)rows * cols + 255) / 256;
+    if (blocks > 65535L * 8) blocks = 65535L * 8;
+    add_bias_kernel<<<(unsigned)blocks, 256, 0, s>>>(out, bias, rows, cols);
+    return (int)hipGetLastError();
+}
 
 int launch_pack_frag16(const void* src, void* dst, int experts, int rows, int cols, hipStream_t s) {
     const long pieces = (long)experts * rows * cols / 8;

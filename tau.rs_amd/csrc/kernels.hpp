@@ -35,6 +35,7 @@ struct GemmArgs {
 
 int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s);
 int launch_pack_frag16(const void* src, void* dst, int experts, int rows, int cols, hipStream_t s);
+int launch_add_bias(float* out, const float* bias, int rows, int cols, hipStream_t s);
 bool gemm_rows_supported(int bm);
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);

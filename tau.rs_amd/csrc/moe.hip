@@ -104,6 +104,16 @@ bool layout_ok(int weight_layout, int hidden, int intermediate) {
 
 extern "C" {
 
+int tau_launch_moe_router_ex(const void* input, const void* weight, const float* bias, float* logits, int tokens,
+                             int hidden, int experts, void* stream) {
+    if (!input || !weight || !logits || tokens <= 0 || tokens > kMaxTokens || hidden <= 0 || experts <= 0 ||
+        experts > 512)
+        return kInvalid;
+    const int code = tau_launch_linear_bf16_fp32(input, weight, logits, tokens, experts, hidden, stream);
+    if (code || !bias) return code;
+    return launch_add_bias(logits, bias, tokens, experts, as_stream(stream));
+}
+
 int tau_moe_pack_weights(const void* src, void* dst, int experts, int rows, int columns, void* stream) {
     if (!src || !dst || src == dst || experts <= 0 || rows <= 0 || columns <= 0 || rows % 16 || columns % 64 ||
         (long)experts * rows * columns / 8 > INT_MAX)

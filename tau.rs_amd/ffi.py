@@ -38,6 +38,7 @@ EXPORTS = (
     "tau_launch_moe_shared_expert_ex",
     "tau_launch_moe_grouped_gemm_ex",
     "tau_moe_pack_weights",
+    "tau_launch_moe_router_ex",
     "tau_moe_build_target",
 )
 
@@ -97,6 +98,7 @@ def lib():
         "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, i, p],
         "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
         "tau_moe_pack_weights": [p, p, i, i, i, p],
+        "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
     }
     for name, args in sig.items():
         fn = getattr(L, name)
@@ -213,3 +215,10 @@ def pack_weights(w: torch.Tensor, stream=None) -> torch.Tensor:
     check(lib().tau_moe_pack_weights(ptr(w), ptr(out), e, n, k, stream_ptr(stream)), "MoE weight pack")
     return out
 
+
+def router_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor, stream=None):
+    """logits f32 [T, E] = x BF16 [T, H] . weight BF16 [E, H]^T (+ bias f32 [E])."""
+    t, h = x.shape
+    e = weight.shape[0]
+    check(lib().tau_launch_moe_router_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), t, h, e, stream_ptr(stream)),
+          "MoE router")

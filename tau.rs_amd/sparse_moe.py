@@ -223,12 +223,26 @@ class MoePrefillRunner:
 
 
 class SparseMoeBlock:
-    """Routed experts plus the optional always-on shared expert."""
+    """Routed experts plus the optional always-on shared expert (sparse_moe.rs:102-251).
+
+    With `router_weight` (BF16 [E, H]) and optional `router_bias` (f32 [E]) the
+    block computes its own router logits in f32 (routing.rs:91-93) when
+    `forward` is called without them."""
 
     def __init__(self, config: SparseMoeConfig, gate_up, down, shared_gate_up=None, shared_down=None,
-                 shared_gate=None, tile_rows: Optional[int] = None, weight_layout: str = "auto"):
+                 shared_gate=None, tile_rows: Optional[int] = None, weight_layout: str = "auto",
+                 router_weight: Optional[torch.Tensor] = None, router_bias: Optional[torch.Tensor] = None):
         self.runner = MoePrefillRunner(config, gate_up, down, tile_rows, weight_layout)
         self.config = config
+        self.router = None
+        if router_weight is not None:
+            E, H = config.num_experts, config.hidden_size
+            if router_weight.shape != (E, H) or router_weight.dtype != torch.bfloat16:
+                raise ValueError("router weight must be BF16 [num_experts, hidden]")
+            if router_bias is not None and (router_bias.shape != (E,) or router_bias.dtype != torch.float32):
+                raise ValueError("router bias must be f32 [num_experts]")
+            self.router = (router_weight.contiguous(), None if router_bias is None else router_bias.contiguous())
+        self._logits = None
         self.shared = None
         if config.shared_expert is not None:
             if shared_gate_up is None or shared_down is None:
@@ -244,7 +258,20 @@ class SparseMoeBlock:
             self.shared = (gu, dn, shared_gate.contiguous() if config.shared_expert.gated else None)
         self._shared_ws = None
 
-    def forward(self, x: torch.Tensor, logits: torch.Tensor, stream=None) -> torch.Tensor:
+    def logits(self, x: torch.Tensor, stream=None) -> torch.Tensor:
+        """Router scores f32 [T, E] (x . W_r^T + b)."""
+        if self.router is None:
+            raise ValueError("block built without router weights: pass logits to forward")
+        T, E = x.shape[0], self.config.num_experts
+        if self._logits is None or self._logits.shape[0] < T:
+            self._logits = torch.empty(_next_pow2(T), E, dtype=torch.float32, device=x.device)
+        out = self._logits[:T]
+        ffi.router_ex(x, self.router[0], self.router[1], out, stream=stream)
+        return out
+
+    def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        if logits is None:
+            logits = self.logits(x, stream=stream)
         routed = self.runner.forward(x, logits, stream=stream)
         if self.shared is None:
             return routed

@@ -1,0 +1,79 @@
+"""Router projection and the whole block from x (run with -m gpu).
+
+tau_launch_moe_router_ex: logits = x . W_r^T (+ b) in f32 (routing.rs:91-93).
+On dyadic operands every product and partial sum is exact in f32, so the GPU
+logits must equal the oracle's f32 linear bit for bit; SparseMoeBlock.forward(x)
+then routes those logits exactly as the oracle does and matches its layer
+output to the north-star tolerance.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def to_np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def dyadic(shape, seed):
+    n = int(np.prod(shape))
+    v = (((np.arange(n) * 17 + seed) % 31).astype(np.float32) - 15.0) / 128.0
+    return v.reshape(shape)
+
+
+@pytest.mark.parametrize("t,h,e,bias", [(33, 144, 8, False), (7, 256, 128, True), (300, 256, 64, True)])
+def test_router_projection_exact_on_dyadic_operands(tau, oracle, t, h, e, bias):
+    say(f"[router] T={t} H={h} E={e} bias={bias}")
+    x = dyadic((t, h), 3)
+    w = dyadic((e, h), 5)
+    b = (np.arange(e, dtype=np.float32) - e / 2) / 64.0 if bias else None
+    xt = torch.tensor(x).to(torch.bfloat16).cuda()
+    wt = torch.tensor(w).to(torch.bfloat16).cuda()
+    bt = torch.tensor(b).cuda() if bias else None
+    logits = torch.empty(t, e, dtype=torch.float32, device="cuda")
+    tau.ffi.router_ex(xt, wt, bt, logits)
+    torch.cuda.synchronize()
+    ref = oracle.linear(x, w)
+    if bias:
+        ref = ref + b[None, :]
+    np.testing.assert_array_equal(to_np(logits), ref)
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("name", ["c2_30b_a3b_decode", "c3_30b_a3b_prefill"])
+def test_block_forward_from_hidden_states(tau, oracle, name):
+    shape = tau.inputs.CONFIGS[name]
+    if shape.tokens > 256:
+        shape = tau.inputs.scaled(shape, 256)
+    say(f"[block from x] {shape.name}")
+    layer = tau.inputs.make_layer(shape)
+    w_r = layer["router"].to(torch.bfloat16)
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
+    blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], router_weight=w_r, router_bias=layer["bias"])
+    out = blk.forward(layer["x"])
+    torch.cuda.synchronize()
+    x = to_np(layer["x"])
+    logits = to_np(blk._logits[: shape.tokens])
+    ref_logits = oracle.linear(x, to_np(w_r)) + to_np(layer["bias"])[None, :]
+    err = np.abs(logits - ref_logits)
+    assert np.all(err <= 1e-5 * np.abs(ref_logits) + 1e-5), float(err.max())  # f32 order differences only
+    K = shape.top_k
+    ids, w = oracle.route(logits, K)
+    routes = to_np(blk.runner.plan_views(shape.tokens)["routes"])
+    np.testing.assert_array_equal(routes[:, :K].astype(np.int64), ids)
+    ref = oracle.moe(x, ids, w, to_np(layer["gate_up"]), to_np(layer["down"]))
+    e = rel_l2(to_np(out), ref)
+    say(f"    rel_l2 vs f32 oracle {e:.2e}")
+    assert e <= 1e-2
