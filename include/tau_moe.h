@@ -150,19 +150,23 @@ int tau_launch_moe_prefill_dispatch_ex(const void* logits, int logits_dtype, flo
                                        int* offsets, int* slots, int* tiles, int tokens, int experts, int top_k,
                                        int tile_rows, int capacity, void* stream);
 
-/* Rank-ordered combine: output[t] = bf16(sum_r contributions[t*K + r]). */
+/* Rank-ordered combine: output[t] = bf16(sum_r contributions[t*K + r]); with a
+ * residual (BF16 [T,H], may be NULL) output = bf16(f32(that) + residual), the
+ * layer's residual add (qwen3_5_common/decoder.rs:96-116) fused. */
 int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, const int* meta, int tokens,
-                                      int hidden, int experts, int top_k, void* stream);
+                                      int hidden, int experts, int top_k, const void* residual, void* stream);
 
 /* Whole routed path for any (E, K): routing, dispatch, gate_up+SiLU·mul,
  * down+weight, combine.  tile_rows from tau_moe_select_tile_rows (or any of
  * 16/32/64/128/256); weight_layout TAU_MOE_WEIGHTS_* for both weight tensors;
- * receipts (optional) receive 10 words, gate_up then down. */
+ * residual (may be NULL) is added in the combine as above (pass it here only
+ * when no shared expert follows); receipts (optional) receive 10 words,
+ * gate_up then down. */
 int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_dtype, const void* gate_up,
                               const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                               void* activated, void* contributions, void* output, int tokens, int hidden,
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                              int weight_layout, int* receipts, void* stream);
+                              int weight_layout, const void* residual, int* receipts, void* stream);
 
 /* One grouped projection over an existing dispatch (meta/slots/tiles from
  * tau_launch_moe_prefill_dispatch_ex with the same tile_rows):
@@ -179,11 +183,13 @@ int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* ro
  * tokens with gate_up_s BF16 [2Is,H], down_s BF16 [Is,H]^T = [H,Is], then
  * output = bf16(fma(sigmoid(x . gate_weight), shared, routed)) (gate_weight
  * may be NULL for an ungated expert).  activated_ws BF16 [T,Is], shared_ws
- * BF16 [T,H].  `output` may alias `routed`. */
+ * BF16 [T,H].  `output` may alias `routed`.  residual (BF16 [T,H], may be NULL):
+ * output = bf16(f32(bf16(fma(...))) + residual), the fused residual add. */
 int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, const void* down_s,
                                     const void* gate_weight, const void* routed, void* activated_ws,
                                     void* shared_ws, void* output, int tokens, int hidden,
-                                    int shared_intermediate, int weight_layout, void* stream);
+                                    int shared_intermediate, int weight_layout, const void* residual,
+                                    void* stream);
 
 /* Router projection (routing.rs:91-93, Router::logits; bias of config.rs:37-78):
  * logits f32 [T, E] = input BF16 [T, H] . weight BF16 [E, H]^T (+ bias f32 [E],

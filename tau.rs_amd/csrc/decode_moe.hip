@@ -248,8 +248,8 @@ bool decode_path_supported(int tokens, int hidden, int intermediate, int experts
 int launch_decode_moe(const void* input, const void* logits, int logits_dtype, const void* gate_up,
                       const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                       void* activated, void* contributions, void* output, int tokens, int hidden,
-                      int intermediate, int experts, int top_k, int capacity, int weight_layout, int* receipts,
-                      hipStream_t s) {
+                      int intermediate, int experts, int top_k, int capacity, int weight_layout,
+                      const void* residual, int* receipts, hipStream_t s) {
     if (!decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout)) return kInvalid;
     int code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
     if (code) return code;
@@ -315,7 +315,7 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
         code = launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsRowMajor, true>(d, plan, plan_lds, s);
     }
     if (code) return code;
-    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, s);
+    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, residual, s);
 }
 
 }  // namespace tau_amd

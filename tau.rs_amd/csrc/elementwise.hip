@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const T* in, T* out, 
 // shared expert (gate = 1).
 __global__ __launch_bounds__(256) void shared_combine_kernel(const uint16_t* x, const uint16_t* w,
                                                              const uint16_t* shared, const uint16_t* routed,
-                                                             uint16_t* out, int width) {
+                                                             uint16_t* out, int width, const uint16_t* residual) {
     __shared__ float partial[4];
     const long row = (long)blockIdx.x * width;
     float gate = 1.0f;
@@ -54,9 +54,11 @@ __global__ __launch_bounds__(256) void shared_combine_kernel(const uint16_t* x, 
         __syncthreads();
         gate = sigmoid((partial[0] + partial[1]) + (partial[2] + partial[3]));
     }
-    for (int c = threadIdx.x; c < width; c += 256)
-        out[row + c] = float_to_bf16_bits(
-            fmaf(gate, bf16_bits_to_float(shared[row + c]), bf16_bits_to_float(routed[row + c])));
+    for (int c = threadIdx.x; c < width; c += 256) {
+        float v = fmaf(gate, bf16_bits_to_float(shared[row + c]), bf16_bits_to_float(routed[row + c]));
+        if (residual) v = round_bf16(v) + bf16_bits_to_float(residual[row + c]);  // fused residual add
+        out[row + c] = float_to_bf16_bits(v);
+    }
 }
 
 // Row-major W[e][rows][cols] -> frag16: 16-byte piece p of the output holds
@@ -118,10 +120,11 @@ int launch_silu_and_mul(const void* in, void* out, int rows, int columns, int dt
 }
 
 int launch_shared_combine(const void* x, const void* w, const void* shared, const void* routed, void* out,
-                          int rows, int width, hipStream_t s) {
+                          int rows, int width, const void* residual, hipStream_t s) {
     if (!x || !shared || !routed || !out || rows <= 0 || width <= 0) return kInvalid;
     shared_combine_kernel<<<rows, 256, 0, s>>>((const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)shared,
-                                               (const uint16_t*)routed, (uint16_t*)out, width);
+                                               (const uint16_t*)routed, (uint16_t*)out, width,
+                                               (const uint16_t*)residual);
     return (int)hipGetLastError();
 }
 

@@ -45,7 +45,7 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
                     int* tiles, int tokens, int E, int K, int M, int capacity, void* scratch, size_t scratch_bytes,
                     hipStream_t s);
 int launch_combine(const void* contributions, void* output, const int* status, int tokens, int H, int K,
-                   hipStream_t s);
+                   const void* residual, hipStream_t s);
 
 // Fused decode path (decode_moe.hip): same outputs as routing + dispatch +
 // grouped GEMMs + combine with 16-row blocks, the plan built off the critical
@@ -55,7 +55,7 @@ bool decode_path_supported(int tokens, int hidden, int intermediate, int experts
 int launch_decode_moe(const void* input, const void* logits, int logits_dtype, const void* gate_up,
                       const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                       void* activated, void* contributions, void* output, int tokens, int hidden,
-                      int intermediate, int experts, int top_k, int capacity, int weight_layout, int* receipts,
-                      hipStream_t s);
+                      int intermediate, int experts, int top_k, int capacity, int weight_layout,
+                      const void* residual, int* receipts, hipStream_t s);
 
 }  // namespace tau_amd

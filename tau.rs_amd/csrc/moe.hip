@@ -13,7 +13,7 @@
 namespace tau_amd {
 int launch_silu_and_mul(const void* in, void* out, int rows, int columns, int dtype, hipStream_t s);
 int launch_shared_combine(const void* x, const void* w, const void* shared, const void* routed, void* out,
-                          int rows, int width, hipStream_t s);
+                          int rows, int width, const void* residual, hipStream_t s);
 }  // namespace tau_amd
 
 using namespace tau_amd;
@@ -185,15 +185,16 @@ int tau_launch_moe_prefill_dispatch(const float* routes, int* meta, int* offsets
 }
 
 int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, const int* meta, int tokens,
-                                      int hidden, int experts, int top_k, void* stream) {
+                                      int hidden, int experts, int top_k, const void* residual, void* stream) {
     if (!meta || experts <= 0 || top_k <= 0 || tokens > kMaxTokens) return kInvalid;
-    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, as_stream(stream));
+    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, residual,
+                          as_stream(stream));
 }
 
 int tau_launch_moe_prefill_combine(const void* contributions, void* output, const int* meta, int rows,
                                    int width, void* stream) {
     if (rows <= 0 || rows > 65535) return kInvalid;
-    return tau_launch_moe_prefill_combine_ex(contributions, output, meta, rows, width, kRefExperts, kRefTopK,
+    return tau_launch_moe_prefill_combine_ex(contributions, output, meta, rows, width, kRefExperts, kRefTopK, nullptr,
                                              stream);
 }
 
@@ -228,7 +229,7 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                               const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
                               void* activated, void* contributions, void* output, int tokens, int hidden,
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
-                              int weight_layout, int* receipts, void* stream) {
+                              int weight_layout, const void* residual, int* receipts, void* stream) {
     if (!input || !logits || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
         !contributions || !output || !shape_ok(tokens, hidden, intermediate, experts, top_k) ||
         !layout_ok(weight_layout, hidden, intermediate) ||
@@ -239,7 +240,7 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
     if (decode_path_supported(tokens, hidden, intermediate, experts, top_k, tile_rows, weight_layout))
         return launch_decode_moe(input, logits, logits_dtype, gate_up, down, routes, meta, offsets, slots, tiles,
                                  activated, contributions, output, tokens, hidden, intermediate, experts, top_k,
-                                 capacity, weight_layout, receipts, s);
+                                 capacity, weight_layout, residual, receipts, s);
     // The contributions buffer is free until the down projection: it holds the
     // multi-workgroup dispatch's per-chunk counts.
     int code = launch_dispatch(logits, logits_dtype, routes, meta, offsets, slots, tiles, tokens, experts, top_k,
@@ -254,7 +255,7 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                            hidden, intermediate, receipts ? receipts + 5 : nullptr, weight_layout);
     code = launch_grouped_gemm(d, tile_rows, kADirect, kEpiScatterWeighted, s);
     if (code) return code;
-    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, s);
+    return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, residual, s);
 }
 
 int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* routes, const int* slots,
@@ -289,8 +290,8 @@ int tau_launch_moe_prefill(const void* input, const void* logits, const void* ga
         return kInvalid;
     return tau_launch_moe_prefill_ex(input, logits, 1, gate_up, down, routes, meta, offsets, slots, tiles,
                                      activated, contributions, output, tokens, hidden, intermediate, kRefExperts,
-                                     kRefTopK, gate_up_config->m, capacity, TAU_MOE_WEIGHTS_ROW_MAJOR, receipts,
-                                     stream);
+                                     kRefTopK, gate_up_config->m, capacity, TAU_MOE_WEIGHTS_ROW_MAJOR, nullptr,
+                                     receipts, stream);
 }
 
 int tau_launch_silu_and_mul(const void* input, void* output, int rows, int columns, int dtype, void* stream) {
@@ -300,7 +301,7 @@ int tau_launch_silu_and_mul(const void* input, void* output, int rows, int colum
 int tau_launch_moe_shared_combine(const void* input, const void* weight, const void* shared, const void* routed,
                                   void* output, int rows, int width, void* stream) {
     if (!weight || width > 8192) return kInvalid;
-    return launch_shared_combine(input, weight, shared, routed, output, rows, width, as_stream(stream));
+    return launch_shared_combine(input, weight, shared, routed, output, rows, width, nullptr, as_stream(stream));
 }
 
 int tau_launch_linear_bf16_fp32(const void* input, const void* weight, float* output, int rows, int columns,
@@ -323,7 +324,8 @@ int tau_launch_linear_bf16_fp32(const void* input, const void* weight, float* ou
 int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, const void* down_s,
                                     const void* gate_weight, const void* routed, void* activated_ws,
                                     void* shared_ws, void* output, int tokens, int hidden,
-                                    int shared_intermediate, int weight_layout, void* stream) {
+                                    int shared_intermediate, int weight_layout, const void* residual,
+                                    void* stream) {
     if (!input || !gate_up_s || !down_s || !routed || !activated_ws || !shared_ws || !output || tokens <= 0 ||
         tokens > kMaxTokens || hidden <= 0 || shared_intermediate <= 0 ||
         !layout_ok(weight_layout, hidden, shared_intermediate))
@@ -346,7 +348,7 @@ int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, co
     d.ldo = hidden;
     code = launch_grouped_gemm(d, bm, kADirect, kEpiStoreBf16, s);
     if (code) return code;
-    return launch_shared_combine(input, gate_weight, shared_ws, routed, output, tokens, hidden, s);
+    return launch_shared_combine(input, gate_weight, shared_ws, routed, output, tokens, hidden, residual, s);
 }
 
 }  // extern "C"

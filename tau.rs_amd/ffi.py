@@ -93,9 +93,9 @@ def lib():
         "tau_moe_workspace_bytes": [i, i, i, i, i, i, p],
         "tau_launch_moe_routing_ex": [p, i, p, i, i, i, p],
         "tau_launch_moe_prefill_dispatch_ex": [p, i, p, p, p, p, p, i, i, i, i, i, p],
-        "tau_launch_moe_prefill_combine_ex": [p, p, p, i, i, i, i, p],
-        "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p, p],
-        "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, i, p],
+        "tau_launch_moe_prefill_combine_ex": [p, p, p, i, i, i, i, p, p],
+        "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p, p, p],
+        "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, i, p, p],
         "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
         "tau_moe_pack_weights": [p, p, i, i, i, p],
         "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
@@ -169,24 +169,24 @@ def dispatch_ex(logits, routes, meta, offsets, slots, tiles, tokens, experts, to
 
 
 def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, receipts=None, stream=None,
-               weight_layout=WEIGHTS_ROW_MAJOR):
+               weight_layout=WEIGHTS_ROW_MAJOR, residual=None):
     t, h = x.shape
     i = down.shape[2]
     code = lib().tau_launch_moe_prefill_ex(
         ptr(x), ptr(logits), _dtype_code(logits), ptr(gate_up), ptr(down), ptr(ws["routes"]), ptr(ws["meta"]),
         ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["activated"]),
         ptr(ws["contributions"]), ptr(output), t, h, i, experts, top_k, tile_rows, ws["capacity"],
-        weight_layout, ptr(receipts), stream_ptr(stream))
+        weight_layout, ptr(residual), ptr(receipts), stream_ptr(stream))
     check(code, "MoE grouped prefill")
 
 
 def shared_expert_ex(x, gate_up_s, down_s, gate_weight, routed, activated_ws, shared_ws, output, stream=None,
-                     weight_layout=WEIGHTS_ROW_MAJOR):
+                     weight_layout=WEIGHTS_ROW_MAJOR, residual=None):
     t, h = x.shape
     i_s = down_s.shape[1]
     code = lib().tau_launch_moe_shared_expert_ex(
         ptr(x), ptr(gate_up_s), ptr(down_s), ptr(gate_weight), ptr(routed), ptr(activated_ws), ptr(shared_ws),
-        ptr(output), t, h, i_s, weight_layout, stream_ptr(stream))
+        ptr(output), t, h, i_s, weight_layout, ptr(residual), stream_ptr(stream))
     check(code, "MoE shared expert")
 
 
@@ -199,9 +199,9 @@ def grouped_gemm_ex(a, w, ws, out, tokens, hidden, intermediate, experts, top_k,
     check(code, "MoE grouped GEMM")
 
 
-def combine_ex(contributions, output, meta, tokens, hidden, experts, top_k, stream=None):
+def combine_ex(contributions, output, meta, tokens, hidden, experts, top_k, stream=None, residual=None):
     code = lib().tau_launch_moe_prefill_combine_ex(ptr(contributions), ptr(output), ptr(meta), tokens, hidden,
-                                                   experts, top_k, stream_ptr(stream))
+                                                   experts, top_k, ptr(residual), stream_ptr(stream))
     check(code, "MoE combine")
 
 

@@ -190,7 +190,9 @@ class MoePrefillRunner:
         return self._receipts.view(2, 5).tolist()
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor, out: Optional[torch.Tensor] = None,
-                stream=None) -> torch.Tensor:
+                stream=None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Routed-expert output; with `residual` (BF16 [T, H]) returns
+        bf16(output + residual), the layer's residual add fused in the combine."""
         c = self.config
         if x.dim() != 2 or x.shape[1] != c.hidden_size or x.dtype != torch.bfloat16:
             raise ValueError("input must be BF16 [tokens, hidden]")
@@ -204,7 +206,7 @@ class MoePrefillRunner:
             out = torch.empty_like(x)
         ffi.prefill_ex(x.contiguous(), logits.contiguous(), self.gate_up, self.down, ws, out, c.num_experts,
                        c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream,
-                       weight_layout=self.layout)
+                       weight_layout=self.layout, residual=residual)
         self._calls += 1
         return out
 
@@ -269,12 +271,17 @@ class SparseMoeBlock:
         ffi.router_ex(x, self.router[0], self.router[1], out, stream=stream)
         return out
 
-    def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None,
+                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Block output; with `residual` (BF16 [T, H]) the layer's residual add
+        (decoder.rs:96-116) is fused into the block's last epilogue."""
         if logits is None:
             logits = self.logits(x, stream=stream)
-        routed = self.runner.forward(x, logits, stream=stream)
+        if residual is not None and (residual.shape != x.shape or residual.dtype != torch.bfloat16):
+            raise ValueError("residual must be BF16 shaped like the input")
         if self.shared is None:
-            return routed
+            return self.runner.forward(x, logits, stream=stream, residual=residual)
+        routed = self.runner.forward(x, logits, stream=stream)
         gu, dn, gw = self.shared
         T = x.shape[0]
         Is = self.config.shared_expert.intermediate_size
@@ -284,5 +291,5 @@ class SparseMoeBlock:
                                torch.empty(n, x.shape[1], dtype=torch.bfloat16, device=x.device))
         act, sh = self._shared_ws
         ffi.shared_expert_ex(x, gu, dn, gw, routed, act[:T], sh[:T], routed, stream=stream,
-                             weight_layout=self.shared_layout)
+                             weight_layout=self.shared_layout, residual=residual)
         return routed

@@ -77,3 +77,28 @@ def test_block_forward_from_hidden_states(tau, oracle, name):
     e = rel_l2(to_np(out), ref)
     say(f"    rel_l2 vs f32 oracle {e:.2e}")
     assert e <= 1e-2
+
+
+@pytest.mark.parametrize("which", ["c2", "c3_t256", "c4_t96"])
+def test_fused_residual_equals_separate_bf16_add(tau, which):
+    """forward(x, residual=r) == bf16(f32(forward(x)) + f32(r)) bit for bit, on
+    the fused decode path (c2), the general path (c3) and with the shared
+    expert finishing the block (c4)."""
+    C = tau.inputs.CONFIGS
+    shape = {"c2": C["c2_30b_a3b_decode"], "c3_t256": tau.inputs.scaled(C["c3_30b_a3b_prefill"], 256),
+             "c4_t96": tau.inputs.scaled(C["c4_next_sparse"], 96)}[which]
+    say(f"[residual] {shape.name}")
+    layer = tau.inputs.make_layer(shape)
+    shared = None
+    if shape.shared_intermediate:
+        shared = tau.SharedExpertConfig(shape.shared_intermediate, gated=True)
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k, shared_expert=shared)
+    blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer.get("shared_gate_up"),
+                             layer.get("shared_down"), layer.get("shared_gate"))
+    g = torch.Generator(device="cuda").manual_seed(9)
+    res = torch.randn(layer["x"].shape, generator=g, device="cuda").to(torch.bfloat16)
+    plain = blk.forward(layer["x"], layer["logits"]).clone()
+    fused = blk.forward(layer["x"], layer["logits"], residual=res)
+    torch.cuda.synchronize()
+    expect = (plain.float() + res.float()).to(torch.bfloat16)
+    np.testing.assert_array_equal(fused.view(torch.int16).cpu().numpy(), expect.view(torch.int16).cpu().numpy())

@@ -106,7 +106,9 @@ def test_frag16_entry_points_reject_unsupported_shapes(tau):
     assert L.tau_moe_pack_weights(d, d, 2, 32, 128, None) == 1   # in place
     args = [d] * 13
     # hidden 96 is not a whole number of 64-wide K steps: frag16 rejected
-    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 96, 128, 8, 2, 16, 4096, 1, None, None) == 1
+    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 96, 128, 8, 2, 16, 4096, 1, None, None,
+                                       None) == 1
     # unknown layout code
-    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 128, 128, 8, 2, 16, 4096, 7, None, None) == 1
+    assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 128, 128, 8, 2, 16, 4096, 7, None, None,
+                                       None) == 1
     assert L.tau_launch_moe_grouped_gemm_ex(*([d] * 7), 64, 96, 128, 8, 2, 16, 4096, 0, 1, None, None) == 1
