@@ -293,3 +293,20 @@ class SparseMoeBlock:
         ffi.shared_expert_ex(x, gu, dn, gw, routed, act[:T], sh[:T], routed, stream=stream,
                              weight_layout=self.shared_layout, residual=residual)
         return routed
+
+    def capture(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None,
+                residual: Optional[torch.Tensor] = None):
+        """Records forward(x, logits, residual) into a HIP graph (the reference
+        captures its prepared decode program, components/cuda/graph.rs:22-150).
+
+        x / logits / residual are the graph's static input buffers: copy new
+        values into them and call graph.replay(); the result lands in the
+        returned output tensor.  One eager call first sizes the workspaces, so
+        the capture allocates nothing; the library issues kernels only (no
+        memset nodes).  Returns (graph, output)."""
+        self.forward(x, logits, residual=residual)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = self.forward(x, logits, residual=residual)
+        return graph, out
