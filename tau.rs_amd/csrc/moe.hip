@@ -331,6 +331,9 @@ int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, co
         !layout_ok(weight_layout, hidden, shared_intermediate))
         return kInvalid;
     hipStream_t s = as_stream(stream);
+    // Row blocks of the dense shared GEMMs: weight streaming for decode sizes,
+    // then 128-row MFMA tiles (256-row tiles leave too few workgroups for a
+    // dense GEMM of a few thousand tokens: measured slower at 2048).
     const int bm = tokens <= 16 ? 16 : (tokens <= 64 ? 64 : 128);
     GemmArgs g = gate_up_args(input, gate_up_s, nullptr, nullptr, nullptr, nullptr, activated_ws, tokens, 1,
                               tokens, hidden, shared_intermediate, nullptr, weight_layout);

@@ -391,10 +391,12 @@ def test_fused_single_token_decode(tau, oracle):
     assert rel_l2(f32(bufs["out"]), ref) <= 2e-3
 
 
-def test_shared_expert_path_matches_oracle(tau, oracle):
+@pytest.mark.parametrize("tokens", [96, 300, 600])
+def test_shared_expert_path_matches_oracle(tau, oracle, tokens):
     """Routed + gated shared expert (c4-style) vs the oracle's f32 path
-    (shared_expert.rs:39-69,142-160) and its BF16 contract (moe_shared.cu)."""
-    shape = tau.inputs.scaled(tau.inputs.CONFIGS["c4_next_sparse"], 96)
+    (shared_expert.rs:39-69,142-160) and its BF16 contract (moe_shared.cu);
+    300 and 600 tokens end in partial row blocks of the dense shared GEMMs."""
+    shape = tau.inputs.scaled(tau.inputs.CONFIGS["c4_next_sparse"], tokens)
     say(f"[shared expert] T={shape.tokens}")
     layer = tau.inputs.make_layer(shape)
     cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k,
