@@ -962,7 +962,7 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
 // built tiles[] (one expert per bm rows) and the kernels index it per block.
 // 16/32: weight streaming; 64/128/256: direct-to-LDS
 // MFMA tiles (64x256 with 4 waves, 128x128 with 4 waves, 256x256 with 16
-// waves), measured best on MI355X for the prefill shapes; shapes the MFMA
+// waves, wave tile 64x64), measured best on MI355X for the prefill shapes; shapes the MFMA
 // kernel cannot take (K not a multiple of 64, unaligned rows, FP32 output)
 // use the register-staged LDS kernel, which reads row-major weights only.
 template <int AM, int EPI, int WL>
@@ -973,7 +973,7 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
             switch (bm) {
                 case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(p, s);
                 case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL>(p, s);
-                case 256: return launch_mfma<256, 256, 8, 2, 2, AM, EPI, 64, WL>(p, s);
+                case 256: return launch_mfma<256, 256, 4, 4, 2, AM, EPI, 64, WL>(p, s);
                 default: break;
             }
         }
