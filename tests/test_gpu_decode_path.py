@@ -35,6 +35,24 @@ def cases(tau):
     ]
 
 
+def variants(tau):
+    """Logit edge cases for the rows the gate_up waves rank from the logits:
+    heavy ties (ids break them), FP32 logits, an expert count that is not a
+    multiple of 8 (unvectorised row reads) with K > 16, and a non-finite row
+    (the plan is marked invalid and every output element is NaN)."""
+    MoeShape = tau.inputs.MoeShape
+    return [
+        ("ties_bf16", MoeShape("ties", 256, 128, 8, 128, 64, 11), "frag16", "ties", torch.bfloat16),
+        ("ties_f32", MoeShape("ties32", 256, 128, 8, 128, 40, 12), "row_major", "ties", torch.float32),
+        ("f32_logits", MoeShape("f32", 512, 64, 6, 192, 33, 13), "frag16", None, torch.float32),
+        ("e60_k20", MoeShape("e60", 256, 60, 20, 128, 24, 14), "row_major", None, torch.bfloat16),
+        ("e60_k20_f32", MoeShape("e60f", 256, 60, 20, 128, 24, 15), "frag16", "ties", torch.float32),
+        ("e250_k3", MoeShape("e250", 256, 250, 3, 64, 64, 16), "frag16", None, torch.bfloat16),
+        ("nan_row", MoeShape("nan", 256, 128, 8, 128, 8, 17), "frag16", "nan", torch.bfloat16),
+        ("inf_row_f32", MoeShape("inf", 256, 32, 4, 64, 5, 18), "row_major", "inf", torch.float32),
+    ]
+
+
 @pytest.mark.parametrize("idx", range(6))
 def test_decode_path_matches_general_path(tau, idx):
     name, shape, layout = cases(tau)[idx]
@@ -43,6 +61,29 @@ def test_decode_path_matches_general_path(tau, idx):
         shape = dataclasses.replace(shape, experts=256, shared_intermediate=0)
     say(f"[decode path] {name} T={shape.tokens} E={shape.experts} K={shape.top_k} {layout}")
     layer = tau.inputs.make_layer(shape)
+    compare_paths(tau, shape, layer, layout)
+
+
+@pytest.mark.parametrize("idx", range(8))
+def test_decode_path_logit_edge_cases(tau, idx):
+    name, shape, layout, edit, dtype = variants(tau)[idx]
+    say(f"[decode path] {name} T={shape.tokens} E={shape.experts} K={shape.top_k} {layout} {dtype}")
+    layer = tau.inputs.make_layer(shape)
+    lg = layer["x"].float() @ layer["router"].t()
+    if edit == "ties":  # a coarse grid: many equal logits per row
+        lg = torch.round(lg * 4) / 4
+    elif edit == "nan":
+        lg[3, 5] = float("nan")
+    elif edit == "inf":
+        lg[2, 0] = float("inf")
+    layer["logits"] = lg.to(dtype).contiguous()
+    if edit == "ties":
+        row = layer["logits"][0].float()
+        assert len(torch.unique(row)) < shape.experts  # the grid really ties
+    compare_paths(tau, shape, layer, layout)
+
+
+def compare_paths(tau, shape, layer, layout):
     T, H, I, E, K = shape.tokens, shape.hidden, shape.intermediate, shape.experts, shape.top_k
     cfg = tau.SparseMoeConfig(H, I, E, K)
     runner = tau.MoePrefillRunner(cfg, layer["gate_up"], layer["down"], 16, weight_layout=layout)
