@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--tile-rows", type=int, default=0, help="override the library's row-block choice")
     ap.add_argument("--weight-layout", choices=("auto", "row_major", "frag16"), default="auto",
                     help="expert weight layout held by the runner (auto: FRAG16 when the shape allows)")
+    ap.add_argument("--with-norm", action="store_true",
+                    help="time the decoder's feed-forward half: fused residual add + centered RMSNorm, then the "
+                         "MoE layer with the final residual add fused into its combine")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
@@ -68,9 +71,16 @@ def parse():
 class Layer:
     """One workload: inputs, rotating weight banks and a dispatch workspace."""
 
-    def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto"):
+    def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto", with_norm=False):
         self.tau, self.torch, self.shape = tau, torch, shape
         self.data = tau.inputs.make_layer(shape)
+        self.norm = None
+        if with_norm:  # attention-branch output, norm weight, residual and normalized buffers
+            g = torch.Generator(device="cuda").manual_seed(shape.seed + 100)
+            x = self.data["x"]
+            self.norm = (torch.randn(x.shape, generator=g, device="cuda").to(torch.bfloat16),
+                         (torch.randn(shape.hidden, generator=g, device="cuda") * 0.1).to(torch.bfloat16),
+                         torch.empty_like(x), torch.empty_like(x))
         cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
         # The runner prepares the weights once (load time): FRAG16 copies when
         # the shape allows, as a serving deployment would hold them.
@@ -95,15 +105,30 @@ class Layer:
         self.out = torch.empty_like(self.data["x"])
         self.receipts = torch.zeros(10, dtype=torch.int32, device="cuda")
 
+    def residual_norm(self, i=0):
+        """residual = x + branch (BF16), normalized = centered RMSNorm(residual)."""
+        branch, w, res, normed = self.norm
+        x = self.data["x"]
+        ffi = self.tau.ffi
+        ffi.check(ffi.lib().tau_launch_fused_residual_rms_norm(
+            ffi.ptr(x), ffi.ptr(branch), ffi.ptr(w), ffi.ptr(res), ffi.ptr(normed), x.shape[0], x.shape[1], 1e-6, 1,
+            ffi.stream_ptr(), 16), "fused residual RMSNorm")
+
     def step(self, i):
         gu, dn = self.banks[i % len(self.banks)]
         s = self.shape
-        self.tau.ffi.prefill_ex(self.data["x"], self.data["logits"], gu, dn, self.ws, self.out, s.experts,
-                                s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout)
+        x, residual = self.data["x"], None
+        if self.norm is not None:
+            self.residual_norm()
+            x, residual = self.norm[3], self.norm[2]
+        # the residual add finishes the block: in the combine, or in the shared combine when there is one
+        self.tau.ffi.prefill_ex(x, self.data["logits"], gu, dn, self.ws, self.out, s.experts,
+                                s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout,
+                                residual=residual if self.shared is None else None)
         if self.shared is not None:
             gu_s, dn_s, gate, lay, act, sh = self.shared
-            self.tau.ffi.shared_expert_ex(self.data["x"], gu_s, dn_s, gate, self.out, act, sh, self.out,
-                                          weight_layout=lay)
+            self.tau.ffi.shared_expert_ex(x, gu_s, dn_s, gate, self.out, act, sh, self.out,
+                                          weight_layout=lay, residual=residual)
 
     def projection(self, i, which):
         gu, dn = self.banks[i % len(self.banks)]
@@ -212,7 +237,7 @@ def main():
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
-    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout)
+    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm)
 
     for i in range(args.warmup):
         layer.step(i)
@@ -251,6 +276,15 @@ def main():
         gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e12, dn_alg / (ms_dn * 1e-3) / 1e12
         unit, peak, bound = "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "mfma"
         traffic_alg = (gu_alg, dn_alg)
+    norm_report = None
+    if layer.norm is not None:
+        # algorithmic bytes: read x and branch, write residual and normalized (BF16), read the weight
+        norm_bytes = 4 * T * H * 2 + H * 2
+        layer.residual_norm()
+        torch.cuda.synchronize()
+        ms_norm = time_events(torch, layer.residual_norm, n_proj)
+        norm_report = {"us": ms_norm * 1e3, "bytes": norm_bytes, "GB/s": norm_bytes / (ms_norm * 1e-3) / 1e9,
+                       "hbm_frac": norm_bytes / (ms_norm * 1e-3) / 1e9 / HBM_PEAK_GBS}
     dominant = "gate_up" if ms_gu >= ms_dn else "down"
     achieved = gu_rate if dominant == "gate_up" else dn_rate
 
@@ -274,7 +308,7 @@ def main():
         "config": {
             "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
-            "weight_layout": layout_name,
+            "weight_layout": layout_name, "feed_forward_half": layer.norm is not None,
             "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
         "roofline": {
@@ -289,6 +323,7 @@ def main():
             "algorithmic_bytes": bytes_, "algorithmic_flops": flops,
         },
         "wall_s_timed": wall,
+        **({"residual_norm": norm_report} if norm_report else {}),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -198,6 +198,31 @@ int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, co
 int tau_launch_moe_router_ex(const void* input, const void* weight, const float* bias, float* logits, int tokens,
                              int hidden, int experts, void* stream);
 
+/* Replaces tau_launch_fused_residual_rms_norm (cuda_ffi.rs:210-222;
+ * centered_rms_norm.cu:545-565): the decoder layer's post-attention residual
+ * add and centered RMSNorm in front of the MoE block (decoder.rs:103-116).
+ * residual_output = input + branch rounded in the storage dtype;
+ * output = (residual * 1/sqrt(mean(residual^2) + epsilon)) * (1 + weight), f32
+ * arithmetic, rounded once.  input/branch/residual_output/output [rows, columns],
+ * weight [columns]; dtype 0 = f32, 1 = BF16; epsilon > 0 and finite;
+ * preferred_bytes 0, 4, 8 or 16 caps the access width (results do not depend
+ * on it).  Inputs are not modified; the outputs must not overlap them (input
+ * and branch may be the same buffer). */
+int tau_launch_fused_residual_rms_norm(const void* input, const void* branch, const void* weight,
+                                       void* residual_output, void* output, int rows, int columns, float epsilon,
+                                       int dtype, void* stream, int preferred_bytes);
+
+/* Replaces tau_launch_centered_rms_norm_configured (cuda_ffi.rs:231-241;
+ * centered_rms_norm.cu:445-508): the same normalization without the add. */
+int tau_launch_centered_rms_norm_configured(const void* input, const void* weight, void* output, int rows,
+                                            int columns, float epsilon, int dtype, void* stream,
+                                            int preferred_bytes);
+
+/* Replaces tau_launch_centered_rms_norm (centered_rms_norm.cu:511-516): the
+ * configured form with preferred_bytes = 16. */
+int tau_launch_centered_rms_norm(const void* input, const void* weight, void* output, int rows, int columns,
+                                 float epsilon, int dtype, void* stream);
+
 /* Load-time weight preparation (no reference counterpart: the reference's
  * kernels read its packed [E, n, k] storage directly, sparse_moe/experts.rs:
  * 50-90).  Writes the FRAG16 form of row-major src [experts, rows, columns]

@@ -447,3 +447,37 @@ void oracle_silu_and_mul(const float* in, float* out, int rows, int columns, int
             out[(size_t)r * columns + c] = bf16 ? bf16_round(v) : v;
         }
 }
+
+/* Centered RMSNorm, the f32 CPU path of CenteredRmsNorm (rms_norm.rs:107-150;
+ * normalize_in_f32 at :204-210): per row, sum of squares in f32 (each square
+ * rounded, then a sequential sum), mean = sum / cols, inv = 1 / sqrt(mean + eps),
+ * y = (x * inv) * (1 + w), rounded to BF16 when bf16.  With a branch, the row
+ * is first input + branch rounded in the storage dtype (the unfused pair of
+ * rms_norm.rs:66-74, a Candle add in that dtype), written to residual_out. */
+void oracle_centered_rms_norm(const float* input, const float* branch, const float* weight,
+                              float* residual_out, float* out, int rows, int cols, float eps, int bf16) {
+    float* row = (float*)malloc(sizeof(float) * (size_t)cols);
+    for (int r = 0; r < rows; ++r) {
+        const size_t o = (size_t)r * cols;
+        for (int c = 0; c < cols; ++c) {
+            float v = input[o + c];
+            if (branch) {
+                v = v + branch[o + c];
+                if (bf16) v = bf16_round(v);
+            }
+            row[c] = v;
+            if (residual_out) residual_out[o + c] = v;
+        }
+        float ss = 0.0f;
+        for (int c = 0; c < cols; ++c) {
+            const float sq = row[c] * row[c];
+            ss = ss + sq;
+        }
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+        for (int c = 0; c < cols; ++c) {
+            const float y = (row[c] * inv) * (1.0f + weight[c]);
+            out[o + c] = bf16 ? bf16_round(y) : y;
+        }
+    }
+    free(row);
+}

@@ -16,6 +16,7 @@ Every function here forwards to the C restatement documented in
 * ``dense_mlp``        mlp.rs forward (shared expert MLP)
 * ``shared_combine_*`` shared_expert.rs:68,142-159 / moe_shared.cu:17-36
 * ``silu_and_mul``     silu_and_mul.cu:51-76
+* ``centered_rms_norm`` rms_norm.rs:66-74,107-150,204-210 (optional residual add)
 """
 from __future__ import annotations
 
@@ -73,6 +74,8 @@ def lib():
         _lib.oracle_bf16_round_array.argtypes = [f, f, i64]
         _lib.oracle_bf16_round_array.restype = None
         _lib.oracle_set_threads.argtypes = [i]
+        _lib.oracle_centered_rms_norm.argtypes = [f, f, f, f, f, i, i, ctypes.c_float, i]
+        _lib.oracle_centered_rms_norm.restype = None
         _lib.oracle_max_threads.restype = i
     return _lib
 
@@ -234,3 +237,18 @@ def linear(input_, weight) -> np.ndarray:
     out = np.zeros((a.shape[0], b.shape[0]), dtype=np.float32)
     lib().oracle_linear_f32(_p(a), _p(b), _p(out), a.shape[0], b.shape[0], a.shape[1])
     return out
+
+
+def centered_rms_norm(x, weight, eps: float, branch=None, bf16: bool = False):
+    """(residual, normalized) of the f32 CPU path; residual is None without a
+    branch.  Inputs hold values representable in the storage dtype."""
+    x = _f32(x)
+    rows, cols = x.reshape(-1, x.shape[-1]).shape
+    w = _f32(weight).reshape(-1)
+    b = _f32(branch) if branch is not None else None
+    out = np.zeros_like(x)
+    res = np.zeros_like(x) if b is not None else None
+    lib().oracle_centered_rms_norm(_p(x), _p(b) if b is not None else None, _p(w),
+                                   _p(res) if res is not None else None, _p(out), rows, cols, float(eps),
+                                   int(bool(bf16)))
+    return res, out

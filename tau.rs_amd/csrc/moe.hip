@@ -14,6 +14,8 @@ namespace tau_amd {
 int launch_silu_and_mul(const void* in, void* out, int rows, int columns, int dtype, hipStream_t s);
 int launch_shared_combine(const void* x, const void* w, const void* shared, const void* routed, void* out,
                           int rows, int width, const void* residual, hipStream_t s);
+int launch_residual_norm(const void* input, const void* branch, const void* weight, void* residual_out, void* out,
+                         int rows, int columns, float eps, int dtype, int preferred_bytes, hipStream_t s);
 }  // namespace tau_amd
 
 using namespace tau_amd;
@@ -352,6 +354,26 @@ int tau_launch_moe_shared_expert_ex(const void* input, const void* gate_up_s, co
     code = launch_grouped_gemm(d, bm, kADirect, kEpiStoreBf16, s);
     if (code) return code;
     return launch_shared_combine(input, gate_weight, shared_ws, routed, output, tokens, hidden, residual, s);
+}
+
+int tau_launch_fused_residual_rms_norm(const void* input, const void* branch, const void* weight,
+                                       void* residual_output, void* output, int rows, int columns, float epsilon,
+                                       int dtype, void* stream, int preferred_bytes) {
+    if (!branch || !residual_output) return kInvalid;
+    return launch_residual_norm(input, branch, weight, residual_output, output, rows, columns, epsilon, dtype,
+                                preferred_bytes, as_stream(stream));
+}
+
+int tau_launch_centered_rms_norm_configured(const void* input, const void* weight, void* output, int rows,
+                                            int columns, float epsilon, int dtype, void* stream,
+                                            int preferred_bytes) {
+    return launch_residual_norm(input, nullptr, weight, nullptr, output, rows, columns, epsilon, dtype,
+                                preferred_bytes, as_stream(stream));
+}
+
+int tau_launch_centered_rms_norm(const void* input, const void* weight, void* output, int rows, int columns,
+                                 float epsilon, int dtype, void* stream) {
+    return tau_launch_centered_rms_norm_configured(input, weight, output, rows, columns, epsilon, dtype, stream, 16);
 }
 
 }  // extern "C"

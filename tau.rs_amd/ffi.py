@@ -39,6 +39,9 @@ EXPORTS = (
     "tau_launch_moe_grouped_gemm_ex",
     "tau_moe_pack_weights",
     "tau_launch_moe_router_ex",
+    "tau_launch_fused_residual_rms_norm",
+    "tau_launch_centered_rms_norm_configured",
+    "tau_launch_centered_rms_norm",
     "tau_moe_build_target",
 )
 
@@ -76,7 +79,7 @@ def lib():
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (no fallback exists)")
     L = ctypes.CDLL(LIB_PATH)
-    p, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    p, i, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
     sig = {
         "tau_launch_moe_routing_fp32": [p, p, i, p],
         "tau_launch_moe_prefill_dispatch": [p, p, p, p, p, i, i, i, p],
@@ -99,6 +102,9 @@ def lib():
         "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
         "tau_moe_pack_weights": [p, p, i, i, i, p],
         "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
+        "tau_launch_fused_residual_rms_norm": [p, p, p, p, p, i, i, f32, i, p, i],
+        "tau_launch_centered_rms_norm_configured": [p, p, p, i, i, f32, i, p, i],
+        "tau_launch_centered_rms_norm": [p, p, p, i, i, f32, i, p],
     }
     for name, args in sig.items():
         fn = getattr(L, name)
@@ -222,3 +228,39 @@ def router_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor,
     e = weight.shape[0]
     check(lib().tau_launch_moe_router_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), t, h, e, stream_ptr(stream)),
           "MoE router")
+
+
+def _norm_operands(x: torch.Tensor, weight: torch.Tensor):
+    if (x.dim() < 1 or weight.dim() != 1 or x.shape[-1] != weight.numel() or x.dtype != weight.dtype
+            or not x.is_contiguous() or not weight.is_contiguous()):
+        raise ValueError("norm input must be contiguous [..., columns] with a contiguous [columns] weight of its dtype")
+    columns = x.shape[-1]
+    return x.numel() // columns, columns, _dtype_code(x)
+
+
+def centered_rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float, out=None, preferred_bytes: int = 16,
+                      stream=None) -> torch.Tensor:
+    """(x / sqrt(mean(x^2) + eps)) * (1 + weight) over the last dimension, f32
+    arithmetic, rounded once to x's dtype (f32 or BF16)."""
+    rows, columns, dt = _norm_operands(x, weight)
+    out = torch.empty_like(x) if out is None else out
+    check(lib().tau_launch_centered_rms_norm_configured(ptr(x), ptr(weight), ptr(out), rows, columns,
+                                                        float(epsilon), dt, stream_ptr(stream), preferred_bytes),
+          "centered RMSNorm")
+    return out
+
+
+def fused_residual_rms_norm(x: torch.Tensor, branch: torch.Tensor, weight: torch.Tensor, epsilon: float,
+                            preferred_bytes: int = 16, stream=None):
+    """(residual, normalized): residual = x + branch rounded to the dtype, then
+    the centered RMSNorm of the residual; one pass over the rows."""
+    rows, columns, dt = _norm_operands(x, weight)
+    if branch.shape != x.shape or branch.dtype != x.dtype or not branch.is_contiguous():
+        raise ValueError("branch must be contiguous and shaped like the input")
+    residual = torch.empty_like(x)
+    out = torch.empty_like(x)
+    check(lib().tau_launch_fused_residual_rms_norm(ptr(x), ptr(branch), ptr(weight), ptr(residual),
+                                                   ptr(out), rows, columns, float(epsilon), dt, stream_ptr(stream),
+                                                   preferred_bytes),
+          "fused residual RMSNorm")
+    return residual, out

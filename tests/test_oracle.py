@@ -320,3 +320,58 @@ def test_shared_combine_bf16_against_f64_scalar_gate(width):
         gate = np.float64(np.float32(1. / (1. + math.exp(-dot))))
         exp = O.bf16_round((gate * shared[row] + routed[row]).astype(np.float32))
         np.testing.assert_array_equal(got[row], exp)
+
+
+from norm_host import assert_close, f64_norm, patterned, to_dtype  # noqa: E402
+
+
+# --- centered RMSNorm with the residual add (rms_norm.rs:66-150; the reference's
+# norm tests: cuda/rms_norm/tests/residual/{correctness,support}.rs and the f64
+# oracle of cuda/rms_norm/test_support.rs:5-27)
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_norm_oracle_matches_f64_closed_form(bf16):
+    eps = 1e-6
+    for columns in [1, 31, 32, 33, 255, 256, 257, 2560, 5120]:
+        for rows in [1, 5]:
+            x = to_dtype(patterned(rows * columns, 3), bf16).reshape(rows, columns)
+            b = to_dtype(patterned(rows * columns, 19), bf16).reshape(rows, columns)
+            w = to_dtype(patterned(columns, 47), bf16)
+            res, y = O.centered_rms_norm(x, w, eps, branch=b, bf16=bf16)
+            # the residual is the storage-dtype sum (torch's rounding, not the oracle's)
+            np.testing.assert_array_equal(res, to_dtype(x + b, bf16))
+            assert_close(y, f64_norm(res, w, eps), bf16)
+            _, y2 = O.centered_rms_norm(res, w, eps, bf16=bf16)
+            np.testing.assert_array_equal(y, y2)  # fused == norm of the residual
+
+
+def test_norm_oracle_bf16_residual_rounding_known_answers():
+    """residual/correctness.rs:43-91 inputs; the BF16 sums worked by hand:
+    1 + 2^-8 ties to 1 (even), 1 + 3*2^-8 ties to 1 + 2^-6 (even), 1024 - 1024 = 0,
+    bf16(1e4) = bf16(9990) = 9984, bf16(1e-4) = 1.640625 * 2^-14 and
+    bf16(5e-5) = 1.640625 * 2^-15, whose difference is exact."""
+    xin = np.array([1.0, 1.0, -1.0, 0.0, 1024.0, 0.0001, -0.0001, 1e4], np.float32)
+    bin_ = np.array([0.00390625, 0.01171875, -0.00390625, 0.0, -1024.0, -0.00005, 0.00005, -9990.0], np.float32)
+    r5 = 1.640625 * 2.0 ** -15
+    expect = np.array([1.0, 1.015625, -1.0, 0.0, 0.0, r5, -r5, 0.0], np.float32)
+    x = np.tile(to_dtype(xin, True), 320).reshape(1, 2560)
+    b = np.tile(to_dtype(bin_, True), 320).reshape(1, 2560)
+    w = np.tile(to_dtype(np.array([0.0, -1.0, -1.5, 0.25], np.float32), True), 640)
+    for eps in (1e-6, 1e-3):
+        res, y = O.centered_rms_norm(x, w, eps, branch=b, bf16=True)
+        np.testing.assert_array_equal(res.reshape(-1, 8), np.tile(expect, (320, 1)))
+        assert np.all(y.reshape(-1, 4)[:, 1] == 0.0)  # weight -1: the centred scale is exactly zero
+        assert_close(y, f64_norm(res, w, eps), True)
+
+
+def test_norm_oracle_divides_by_width_and_centres_the_scale():
+    # constant rows normalise to +-1 (mean of squares, not their sum)
+    for c in (2.0, -3.0, 0.5):
+        for cols in (4, 100, 2048):
+            _, y = O.centered_rms_norm(np.full((1, cols), c, np.float32), np.zeros(cols, np.float32), 1e-12)
+            assert np.allclose(y, math.copysign(1.0, c), rtol=0, atol=2e-6)
+    # weight w scales by 1 + w
+    x = patterned(64, 5).reshape(1, 64)
+    _, y0 = O.centered_rms_norm(x, np.zeros(64, np.float32), 1e-6)
+    _, y1 = O.centered_rms_norm(x, np.ones(64, np.float32), 1e-6)
+    np.testing.assert_array_equal(y1, y0 * 2)
