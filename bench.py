@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--with-norm", action="store_true",
                     help="time the decoder's feed-forward half: fused residual add + centered RMSNorm, then the "
                          "MoE layer with the final residual add fused into its combine")
+    ap.add_argument("--with-router", action="store_true",
+                    help="start the step from hidden states: the router projection and routing "
+                         "(tau_launch_moe_router_route_ex), then the layer from those routes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
@@ -71,9 +74,14 @@ def parse():
 class Layer:
     """One workload: inputs, rotating weight banks and a dispatch workspace."""
 
-    def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto", with_norm=False):
+    def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto", with_norm=False,
+                 with_router=False):
         self.tau, self.torch, self.shape = tau, torch, shape
         self.data = tau.inputs.make_layer(shape)
+        self.router = None
+        if with_router:  # BF16 router weight, f32 bias, logits output
+            self.router = (self.data["router"].to(torch.bfloat16).contiguous(), self.data["bias"].contiguous(),
+                           torch.empty(shape.tokens, shape.experts, dtype=torch.float32, device="cuda"))
         self.norm = None
         if with_norm:  # attention-branch output, norm weight, residual and normalized buffers
             g = torch.Generator(device="cuda").manual_seed(shape.seed + 100)
@@ -114,6 +122,17 @@ class Layer:
             ffi.ptr(x), ffi.ptr(branch), ffi.ptr(w), ffi.ptr(res), ffi.ptr(normed), x.shape[0], x.shape[1], 1e-6, 1,
             ffi.stream_ptr(), 16), "fused residual RMSNorm")
 
+    def route_from_hidden(self, i=0, x=None):
+        """Router projection (bias fused) and routing into the workspace's routes."""
+        w, b, logits = self.router
+        self.tau.ffi.router_route_ex(self.data["x"] if x is None else x, w, b, logits, self.ws["routes"],
+                                     self.shape.top_k)
+
+    def project_router(self, i=0):
+        """The router projection alone."""
+        w, b, logits = self.router
+        self.tau.ffi.router_ex(self.data["x"], w, b, logits)
+
     def step(self, i):
         gu, dn = self.banks[i % len(self.banks)]
         s = self.shape
@@ -121,8 +140,12 @@ class Layer:
         if self.norm is not None:
             self.residual_norm()
             x, residual = self.norm[3], self.norm[2]
+        logits = self.data["logits"]
+        if self.router is not None:
+            self.route_from_hidden(x=x)
+            logits = None
         # the residual add finishes the block: in the combine, or in the shared combine when there is one
-        self.tau.ffi.prefill_ex(x, self.data["logits"], gu, dn, self.ws, self.out, s.experts,
+        self.tau.ffi.prefill_ex(x, logits, gu, dn, self.ws, self.out, s.experts,
                                 s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout,
                                 residual=residual if self.shared is None else None)
         if self.shared is not None:
@@ -237,7 +260,7 @@ def main():
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
-    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm)
+    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm, args.with_router)
 
     for i in range(args.warmup):
         layer.step(i)
@@ -285,6 +308,13 @@ def main():
         ms_norm = time_events(torch, layer.residual_norm, n_proj)
         norm_report = {"us": ms_norm * 1e3, "bytes": norm_bytes, "GB/s": norm_bytes / (ms_norm * 1e-3) / 1e9,
                        "hbm_frac": norm_bytes / (ms_norm * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    router_report = None
+    if layer.router is not None:
+        layer.route_from_hidden()
+        layer.project_router()
+        torch.cuda.synchronize()
+        router_report = {"projection_and_routing_us": time_events(torch, layer.route_from_hidden, n_proj) * 1e3,
+                         "projection_us": time_events(torch, layer.project_router, n_proj) * 1e3}
     dominant = "gate_up" if ms_gu >= ms_dn else "down"
     achieved = gu_rate if dominant == "gate_up" else dn_rate
 
@@ -309,6 +339,7 @@ def main():
             "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
             "weight_layout": layout_name, "feed_forward_half": layer.norm is not None,
+            "from_hidden_states": layer.router is not None,
             "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
         "roofline": {
@@ -324,6 +355,7 @@ def main():
         },
         "wall_s_timed": wall,
         **({"residual_norm": norm_report} if norm_report else {}),
+        **({"router": router_report} if router_report else {}),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -157,7 +157,8 @@ int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, c
                                       int hidden, int experts, int top_k, const void* residual, void* stream);
 
 /* Whole routed path for any (E, K): routing, dispatch, gate_up+SiLU·mul,
- * down+weight, combine.  tile_rows from tau_moe_select_tile_rows (or any of
+ * down+weight, combine.  logits NULL: `routes` already holds the [T, 2K]
+ * routes (tau_launch_moe_router_route_ex) and routing is skipped.  tile_rows from tau_moe_select_tile_rows (or any of
  * 16/32/64/128/256); weight_layout TAU_MOE_WEIGHTS_* for both weight tensors;
  * residual (may be NULL) is added in the combine as above (pass it here only
  * when no shared expert follows); receipts (optional) receive 10 words,
@@ -222,6 +223,16 @@ int tau_launch_centered_rms_norm_configured(const void* input, const void* weigh
  * configured form with preferred_bytes = 16. */
 int tau_launch_centered_rms_norm(const void* input, const void* weight, void* output, int rows, int columns,
                                  float epsilon, int dtype, void* stream);
+
+/* Router projection and routing in one call, replacing Router::logits
+ * followed by the routing kernel (sparse_moe/routing.rs:91-93,125-231;
+ * moe_routing.cu:15-52 generalised to any E <= 512, K <= 32): logits f32
+ * [T, E] = input BF16 [T, H] . weight BF16 [E, H]^T (+ bias f32 [E], may be
+ * NULL), exactly as tau_launch_moe_router_ex, then softmax / top-K /
+ * renormalised weights into routes [T, 2K] as tau_launch_moe_routing_ex does
+ * from those logits.  Two launches (projection with the bias fused; routing). */
+int tau_launch_moe_router_route_ex(const void* input, const void* weight, const float* bias, float* logits,
+                                   float* routes, int tokens, int hidden, int experts, int top_k, void* stream);
 
 /* Load-time weight preparation (no reference counterpart: the reference's
  * kernels read its packed [E, n, k] storage directly, sparse_moe/experts.rs:

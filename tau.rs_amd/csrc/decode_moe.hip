@@ -251,8 +251,11 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
                       int intermediate, int experts, int top_k, int capacity, int weight_layout,
                       const void* residual, int* receipts, hipStream_t s) {
     if (!decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout)) return kInvalid;
-    int code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
-    if (code) return code;
+    int code = 0;
+    if (logits) {  // otherwise the caller's routes (routing fused with the router projection)
+        code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
+        if (code) return code;
+    }
 
     DispatchArgs plan{};
     plan.routes = routes;

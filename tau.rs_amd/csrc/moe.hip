@@ -14,6 +14,9 @@ namespace tau_amd {
 int launch_silu_and_mul(const void* in, void* out, int rows, int columns, int dtype, hipStream_t s);
 int launch_shared_combine(const void* x, const void* w, const void* shared, const void* routed, void* out,
                           int rows, int width, const void* residual, hipStream_t s);
+bool router_logits_supported(const void* x, const void* w, int hidden, int experts);
+int launch_router_logits(const void* input, const void* weight, const float* bias, float* logits, int tokens,
+                         int hidden, int experts, hipStream_t s);
 int launch_residual_norm(const void* input, const void* branch, const void* weight, void* residual_out, void* out,
                          int rows, int columns, float eps, int dtype, int preferred_bytes, hipStream_t s);
 }  // namespace tau_amd
@@ -106,11 +109,21 @@ bool layout_ok(int weight_layout, int hidden, int intermediate) {
 
 extern "C" {
 
+int tau_launch_moe_router_route_ex(const void* input, const void* weight, const float* bias, float* logits,
+                                   float* routes, int tokens, int hidden, int experts, int top_k, void* stream) {
+    if (!routes || top_k <= 0 || top_k > 32 || top_k > experts) return kInvalid;
+    const int code = tau_launch_moe_router_ex(input, weight, bias, logits, tokens, hidden, experts, stream);
+    if (code) return code;
+    return launch_routing(logits, 0, routes, tokens, experts, top_k, as_stream(stream));
+}
+
 int tau_launch_moe_router_ex(const void* input, const void* weight, const float* bias, float* logits, int tokens,
                              int hidden, int experts, void* stream) {
     if (!input || !weight || !logits || tokens <= 0 || tokens > kMaxTokens || hidden <= 0 || experts <= 0 ||
         experts > 512)
         return kInvalid;
+    if (router_logits_supported(input, weight, hidden, experts))  // skinny-GEMM kernel, bias fused
+        return launch_router_logits(input, weight, bias, logits, tokens, hidden, experts, as_stream(stream));
     const int code = tau_launch_linear_bf16_fp32(input, weight, logits, tokens, experts, hidden, stream);
     if (code || !bias) return code;
     return launch_add_bias(logits, bias, tokens, experts, as_stream(stream));
@@ -232,9 +245,9 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                               void* activated, void* contributions, void* output, int tokens, int hidden,
                               int intermediate, int experts, int top_k, int tile_rows, int capacity,
                               int weight_layout, const void* residual, int* receipts, void* stream) {
-    if (!input || !logits || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
+    if (!input || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
         !contributions || !output || !shape_ok(tokens, hidden, intermediate, experts, top_k) ||
-        !layout_ok(weight_layout, hidden, intermediate) ||
+        !layout_ok(weight_layout, hidden, intermediate) || (logits && logits_dtype != 0 && logits_dtype != 1) ||
         !gemm_rows_supported(tile_rows) || capacity < capacity_for(tokens, experts, top_k, tile_rows) ||
         capacity % tile_rows)
         return kInvalid;

@@ -39,6 +39,7 @@ EXPORTS = (
     "tau_launch_moe_grouped_gemm_ex",
     "tau_moe_pack_weights",
     "tau_launch_moe_router_ex",
+    "tau_launch_moe_router_route_ex",
     "tau_launch_fused_residual_rms_norm",
     "tau_launch_centered_rms_norm_configured",
     "tau_launch_centered_rms_norm",
@@ -102,6 +103,7 @@ def lib():
         "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
         "tau_moe_pack_weights": [p, p, i, i, i, p],
         "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
+        "tau_launch_moe_router_route_ex": [p, p, p, p, p, i, i, i, i, p],
         "tau_launch_fused_residual_rms_norm": [p, p, p, p, p, i, i, f32, i, p, i],
         "tau_launch_centered_rms_norm_configured": [p, p, p, i, i, f32, i, p, i],
         "tau_launch_centered_rms_norm": [p, p, p, i, i, f32, i, p],
@@ -179,7 +181,8 @@ def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, 
     t, h = x.shape
     i = down.shape[2]
     code = lib().tau_launch_moe_prefill_ex(
-        ptr(x), ptr(logits), _dtype_code(logits), ptr(gate_up), ptr(down), ptr(ws["routes"]), ptr(ws["meta"]),
+        ptr(x), ptr(logits), _dtype_code(logits) if logits is not None else 0, ptr(gate_up), ptr(down),
+        ptr(ws["routes"]), ptr(ws["meta"]),
         ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["activated"]),
         ptr(ws["contributions"]), ptr(output), t, h, i, experts, top_k, tile_rows, ws["capacity"],
         weight_layout, ptr(residual), ptr(receipts), stream_ptr(stream))
@@ -220,6 +223,15 @@ def pack_weights(w: torch.Tensor, stream=None) -> torch.Tensor:
     out = torch.empty_like(w)
     check(lib().tau_moe_pack_weights(ptr(w), ptr(out), e, n, k, stream_ptr(stream)), "MoE weight pack")
     return out
+
+
+def router_route_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor, routes: torch.Tensor,
+                    top_k: int, stream=None):
+    """logits f32 [T, E] and routes [T, 2K] from x BF16 [T, H] in one call."""
+    t, h = x.shape
+    e = weight.shape[0]
+    check(lib().tau_launch_moe_router_route_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(routes), t, h, e,
+                                               top_k, stream_ptr(stream)), "MoE router + routing")
 
 
 def router_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor, stream=None):

@@ -189,14 +189,19 @@ class MoePrefillRunner:
     def executed_tiles(self):
         return self._receipts.view(2, 5).tolist()
 
-    def forward(self, x: torch.Tensor, logits: torch.Tensor, out: Optional[torch.Tensor] = None,
-                stream=None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
+                stream=None, residual: Optional[torch.Tensor] = None, router=None) -> torch.Tensor:
         """Routed-expert output; with `residual` (BF16 [T, H]) returns
-        bf16(output + residual), the layer's residual add fused in the combine."""
+        bf16(output + residual), the layer's residual add fused in the combine.
+        logits None: `router` = (weight BF16 [E,H], bias f32 [E] or None,
+        logits_out f32 [T,E] or None) and the router projection runs fused
+        with the routing (tau_launch_moe_router_route_ex)."""
         c = self.config
         if x.dim() != 2 or x.shape[1] != c.hidden_size or x.dtype != torch.bfloat16:
             raise ValueError("input must be BF16 [tokens, hidden]")
-        if logits.shape != (x.shape[0], c.num_experts):
+        if logits is None and router is None:
+            raise ValueError("pass router logits or the router weights")
+        if logits is not None and logits.shape != (x.shape[0], c.num_experts):
             raise ValueError("router logits must be [tokens, num_experts]")
         tokens = x.shape[0]
         tile_rows = self.tile_rows_for(tokens)
@@ -204,7 +209,13 @@ class MoePrefillRunner:
         # Capacity of the allocation covers any token count up to ws["tokens"].
         if out is None:
             out = torch.empty_like(x)
-        ffi.prefill_ex(x.contiguous(), logits.contiguous(), self.gate_up, self.down, ws, out, c.num_experts,
+        x = x.contiguous()
+        if logits is None:
+            w, b, logits_out = router
+            ffi.router_route_ex(x, w, b, logits_out, ws["routes"], c.experts_per_token, stream=stream)
+        else:
+            logits = logits.contiguous()
+        ffi.prefill_ex(x, logits, self.gate_up, self.down, ws, out, c.num_experts,
                        c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream,
                        weight_layout=self.layout, residual=residual)
         self._calls += 1
@@ -271,17 +282,34 @@ class SparseMoeBlock:
         ffi.router_ex(x, self.router[0], self.router[1], out, stream=stream)
         return out
 
+    def _fused_router(self, x: torch.Tensor):
+        """(weight, bias, logits_out) for the router + routing call, or None
+        without router weights."""
+        if self.router is None:
+            return None
+        T, E = x.shape[0], self.config.num_experts
+        if self._logits is None or self._logits.shape[0] < T:
+            self._logits = torch.empty(_next_pow2(T), E, dtype=torch.float32, device=x.device)
+        return self.router[0], self.router[1], self._logits[:T]
+
     def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None,
                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Block output; with `residual` (BF16 [T, H]) the layer's residual add
-        (decoder.rs:96-116) is fused into the block's last epilogue."""
+        (decoder.rs:96-116) is fused into the block's last epilogue.  Without
+        logits the router runs on x together with the routing
+        (tau_launch_moe_router_route_ex; the projection is kept in the block's
+        logits buffer) and the layer starts from those routes."""
+        router = None
         if logits is None:
-            logits = self.logits(x, stream=stream)
+            x = x.contiguous()
+            router = self._fused_router(x)
+            if router is None:
+                raise ValueError("block built without router weights: pass logits to forward")
         if residual is not None and (residual.shape != x.shape or residual.dtype != torch.bfloat16):
             raise ValueError("residual must be BF16 shaped like the input")
         if self.shared is None:
-            return self.runner.forward(x, logits, stream=stream, residual=residual)
-        routed = self.runner.forward(x, logits, stream=stream)
+            return self.runner.forward(x, logits, stream=stream, residual=residual, router=router)
+        routed = self.runner.forward(x, logits, stream=stream, router=router)
         gu, dn, gw = self.shared
         T = x.shape[0]
         Is = self.config.shared_expert.intermediate_size

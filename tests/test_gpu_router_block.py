@@ -102,3 +102,90 @@ def test_fused_residual_equals_separate_bf16_add(tau, which):
     torch.cuda.synchronize()
     expect = (plain.float() + res.float()).to(torch.bfloat16)
     np.testing.assert_array_equal(fused.view(torch.int16).cpu().numpy(), expect.view(torch.int16).cpu().numpy())
+
+
+@pytest.mark.parametrize("t,h,e,k,bias", [(33, 160, 8, 2, False), (17, 96, 20, 4, True), (7, 256, 128, 8, True),
+                                          (300, 256, 64, 6, True), (64, 2048, 128, 8, False),
+                                          (40, 512, 512, 10, True), (5, 64, 256, 32, False)])
+def test_fused_router_routing_exact_on_dyadic_operands(tau, oracle, t, h, e, k, bias):
+    """tau_launch_moe_router_route_ex: the projection exact on dyadic operands,
+    and the routes those logits give under the routing kernel and the oracle,
+    bit for bit."""
+    say(f"[fused router] T={t} H={h} E={e} K={k} bias={bias}")
+    x = dyadic((t, h), 3)
+    w = dyadic((e, h), 5)
+    b = (np.arange(e, dtype=np.float32) - e / 2) / 64.0 if bias else None
+    xt = torch.tensor(x).to(torch.bfloat16).cuda()
+    wt = torch.tensor(w).to(torch.bfloat16).cuda()
+    bt = torch.tensor(b).cuda() if bias else None
+    logits = torch.empty(t, e, dtype=torch.float32, device="cuda")
+    routes = torch.empty(t, 2 * k, dtype=torch.float32, device="cuda")
+    tau.ffi.router_route_ex(xt, wt, bt, logits, routes, k)
+    ref_routes = torch.empty_like(routes)
+    tau.ffi.routing_ex(logits, ref_routes, e, k)
+    torch.cuda.synchronize()
+    ref = oracle.linear(x, w)
+    if bias:
+        ref = ref + b[None, :]
+    np.testing.assert_array_equal(to_np(logits), ref)
+    np.testing.assert_array_equal(to_np(routes), to_np(ref_routes))
+    ids, _ = oracle.route(ref, k)
+    np.testing.assert_array_equal(to_np(routes)[:, :k].astype(np.int64), ids)
+    # the projection is router_ex's, bit for bit (same kernel for H % 32 == 0)
+    logits2 = torch.empty_like(logits)
+    tau.ffi.router_ex(xt, wt, bt, logits2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_np(logits2), to_np(logits))
+
+
+@pytest.mark.parametrize("name", ["c2_30b_a3b_decode", "c3_30b_a3b_prefill", "c5_235b_decode"])
+def test_block_fused_router_equals_block_given_its_logits(tau, name):
+    """forward(x) (router + routing call) == forward(x, logits) on the logits
+    that call produced, bit for bit; the routes agree with the routing
+    kernel's on those logits."""
+    shape = tau.inputs.CONFIGS[name]
+    if shape.tokens > 512:
+        shape = tau.inputs.scaled(shape, 512)
+    say(f"[fused router block] {shape.name}")
+    layer = tau.inputs.make_layer(shape)
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
+    blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], router_weight=layer["router"].to(torch.bfloat16),
+                             router_bias=layer["bias"])
+    fused = blk.forward(layer["x"]).clone()
+    logits = blk._logits[: shape.tokens].clone()
+    routes = blk.runner.plan_views(shape.tokens)["routes"].clone()
+    given = blk.forward(layer["x"], logits)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(fused.view(torch.int16).cpu().numpy(), given.view(torch.int16).cpu().numpy())
+    np.testing.assert_array_equal(to_np(routes), to_np(blk.runner.plan_views(shape.tokens)["routes"]))
+
+
+@pytest.mark.parametrize("t,h,e,k", [(9, 100, 8, 2), (33, 144, 20, 4)])
+def test_router_routing_on_unaligned_hidden_sizes(tau, oracle, t, h, e, k):
+    """H % 32 != 0 (and a misaligned input view): the projection falls back to
+    the general linear kernel; still exact on dyadic operands."""
+    say(f"[router fallback] T={t} H={h} E={e} K={k}")
+    x = dyadic((t, h), 7)
+    w = dyadic((e, h), 9)
+    buf = torch.zeros(t * h + 8, dtype=torch.bfloat16, device="cuda")
+    xt = buf[4: 4 + t * h].view(t, h)
+    xt.copy_(torch.tensor(x).to(torch.bfloat16))
+    wt = torch.tensor(w).to(torch.bfloat16).cuda()
+    logits = torch.empty(t, e, dtype=torch.float32, device="cuda")
+    routes = torch.empty(t, 2 * k, dtype=torch.float32, device="cuda")
+    tau.ffi.router_route_ex(xt, wt, None, logits, routes, k)
+    torch.cuda.synchronize()
+    ref = oracle.linear(x, w)
+    np.testing.assert_array_equal(to_np(logits), ref)
+    ids, _ = oracle.route(ref, k)
+    np.testing.assert_array_equal(to_np(routes)[:, :k].astype(np.int64), ids)
+
+
+def test_router_routing_rejects_bad_arguments(tau):
+    w = torch.zeros(8, 64, dtype=torch.bfloat16, device="cuda")
+    logits = torch.empty(8, 8, dtype=torch.float32, device="cuda")
+    routes = torch.empty(8, 18, dtype=torch.float32, device="cuda")
+    with pytest.raises(tau.ffi.LaunchError):  # K > E
+        tau.ffi.router_route_ex(w, w, None, logits, routes, 9)
+    with pytest.raises(tau.ffi.LaunchError):  # no logits buffer
+        tau.ffi.router_route_ex(w, w, None, None, routes, 2)
