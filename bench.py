@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--with-router", action="store_true",
                     help="start the step from hidden states: the router projection and routing "
                          "(tau_launch_moe_router_route_ex), then the layer from those routes")
+    ap.add_argument("--shared-apart", action="store_true",
+                    help="run a shared expert with its own launches instead of folded into the routed schedule")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
@@ -75,13 +77,27 @@ class Layer:
     """One workload: inputs, rotating weight banks and a dispatch workspace."""
 
     def __init__(self, tau, torch, shape, banks, tile_rows=0, weight_layout="auto", with_norm=False,
-                 with_router=False):
+                 with_router=False, shared_apart=False):
         self.tau, self.torch, self.shape = tau, torch, shape
         self.data = tau.inputs.make_layer(shape)
+        d = self.data
+        # A gated shared expert with the experts' intermediate size runs as expert E
+        # of the routed schedule (every token takes it at rank K, weight sigmoid(x . w_s)).
+        self.folded = bool(shape.shared_intermediate) and shape.shared_intermediate == shape.intermediate \
+            and not shared_apart
+        self.experts = shape.experts + (1 if self.folded else 0)   # as launched
+        self.top_k = shape.top_k + (1 if self.folded else 0)
+        if self.folded:  # router logits then the shared gate logit x . w_s (f32), like the router projection
+            gate = d["x"].float() @ d["shared_gate"].float().reshape(-1, 1)
+            self.logits_ext = torch.cat([d["logits"].float(), gate], 1).contiguous()
         self.router = None
-        if with_router:  # BF16 router weight, f32 bias, logits output
-            self.router = (self.data["router"].to(torch.bfloat16).contiguous(), self.data["bias"].contiguous(),
-                           torch.empty(shape.tokens, shape.experts, dtype=torch.float32, device="cuda"))
+        if with_router:  # BF16 router weight (+ w_s when folded), f32 bias, logits output
+            w, b = d["router"].to(torch.bfloat16), d["bias"]
+            if self.folded:
+                w = torch.cat([w, d["shared_gate"].reshape(1, -1).to(torch.bfloat16)], 0)
+                b = torch.cat([b, torch.zeros(1, device="cuda")])
+            self.router = (w.contiguous(), b.contiguous(),
+                           torch.empty(shape.tokens, self.experts, dtype=torch.float32, device="cuda"))
         self.norm = None
         if with_norm:  # attention-branch output, norm weight, residual and normalized buffers
             g = torch.Generator(device="cuda").manual_seed(shape.seed + 100)
@@ -92,11 +108,18 @@ class Layer:
         cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
         # The runner prepares the weights once (load time): FRAG16 copies when
         # the shape allows, as a serving deployment would hold them.
-        self.runner = tau.MoePrefillRunner(cfg, self.data["gate_up"], self.data["down"], tile_rows=tile_rows or None,
-                                           weight_layout=weight_layout)
+        if self.folded:
+            gu_all = torch.cat([d["gate_up"], d["shared_gate_up"].unsqueeze(0)], 0)
+            dn_all = torch.cat([d["down"], d["shared_down"].unsqueeze(0)], 0)
+            self.runner = tau.MoePrefillRunner(cfg, gu_all, dn_all, tile_rows=tile_rows or None,
+                                               weight_layout=weight_layout, fold_shared=True)
+            del gu_all, dn_all
+        else:
+            self.runner = tau.MoePrefillRunner(cfg, d["gate_up"], d["down"], tile_rows=tile_rows or None,
+                                               weight_layout=weight_layout)
         self.layout = self.runner.layout
         self.shared = None
-        if shape.shared_intermediate:  # the always-on shared expert, gated by sigmoid(x . w_s)
+        if shape.shared_intermediate and not self.folded:  # the shared expert's own launches
             gu_s, dn_s = self.data["shared_gate_up"], self.data["shared_down"]
             lay = tau.ffi.WEIGHTS_ROW_MAJOR
             if self.layout == tau.ffi.WEIGHTS_FRAG16 and shape.shared_intermediate % 64 == 0:
@@ -125,8 +148,12 @@ class Layer:
     def route_from_hidden(self, i=0, x=None):
         """Router projection (bias fused) and routing into the workspace's routes."""
         w, b, logits = self.router
-        self.tau.ffi.router_route_ex(self.data["x"] if x is None else x, w, b, logits, self.ws["routes"],
-                                     self.shape.top_k)
+        x = self.data["x"] if x is None else x
+        if self.folded:
+            self.tau.ffi.router_route_shared_ex(x, w, b, logits, self.ws["routes"], self.shape.experts,
+                                                self.shape.top_k)
+        else:
+            self.tau.ffi.router_route_ex(x, w, b, logits, self.ws["routes"], self.shape.top_k)
 
     def project_router(self, i=0):
         """The router projection alone."""
@@ -144,9 +171,12 @@ class Layer:
         if self.router is not None:
             self.route_from_hidden(x=x)
             logits = None
+        elif self.folded:  # routed top-K plus the shared expert at rank K
+            self.tau.ffi.routing_shared_ex(self.logits_ext, self.ws["routes"], s.experts, s.top_k)
+            logits = None
         # the residual add finishes the block: in the combine, or in the shared combine when there is one
-        self.tau.ffi.prefill_ex(x, logits, gu, dn, self.ws, self.out, s.experts,
-                                s.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout,
+        self.tau.ffi.prefill_ex(x, logits, gu, dn, self.ws, self.out, self.experts,
+                                self.top_k, self.tile_rows, receipts=self.receipts, weight_layout=self.layout,
                                 residual=residual if self.shared is None else None)
         if self.shared is not None:
             gu_s, dn_s, gate, lay, act, sh = self.shared
@@ -160,7 +190,7 @@ class Layer:
             a, w, out = self.data["x"], gu, self.ws["activated"]
         else:
             a, w, out = self.ws["activated"], dn, self.ws["contributions"]
-        self.tau.ffi.grouped_gemm_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, s.experts, s.top_k,
+        self.tau.ffi.grouped_gemm_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, self.experts, self.top_k,
                                      self.tile_rows, which, weight_layout=self.layout)
 
 
@@ -260,7 +290,8 @@ def main():
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
-    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm, args.with_router)
+    layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm, args.with_router,
+                  args.shared_apart)
 
     for i in range(args.warmup):
         layer.step(i)
@@ -271,10 +302,10 @@ def main():
     wall = time.perf_counter() - t0
 
     # Routing facts for the algorithmic work.
-    meta = layer.ws["meta"][: 2 * shape.experts + 2].cpu()
-    counts = meta[: shape.experts]
+    meta = layer.ws["meta"][: 2 * layer.experts + 2].cpu()
+    counts = meta[: shape.experts]  # routed experts (a folded shared expert is expert E)
     distinct = int((counts > 0).sum())
-    status = int(meta[2 * shape.experts])
+    status = int(meta[2 * layer.experts])
     flops, bytes_ = tau.inputs.algorithmic_work(shape, distinct)
 
     # Per-projection timing over the live dispatch (one untimed launch each
@@ -286,11 +317,12 @@ def main():
     ms_gu = time_events(torch, lambda i: layer.projection(i, 0), n_proj)
     ms_dn = time_events(torch, lambda i: layer.projection(i, 1), n_proj)
     T, H, I, K = shape.tokens, shape.hidden, shape.intermediate, shape.top_k
-    A = T * K
+    A = T * layer.top_k  # assignments per launch (a folded shared expert adds T)
+    d_launch = distinct + (1 if layer.folded else 0)
     decode = layer.tile_rows <= 32
     if decode:
-        gu_alg = distinct * 2 * I * H * 2 + T * H * 2 + A * I * 2
-        dn_alg = distinct * H * I * 2 + A * I * 2 + A * H * 2
+        gu_alg = d_launch * 2 * I * H * 2 + T * H * 2 + A * I * 2
+        dn_alg = d_launch * H * I * 2 + A * I * 2 + A * H * 2
         gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e9, dn_alg / (ms_dn * 1e-3) / 1e9
         unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
         traffic_alg = (gu_alg, dn_alg)
@@ -340,6 +372,7 @@ def main():
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
             "weight_layout": layout_name, "feed_forward_half": layer.norm is not None,
             "from_hidden_states": layer.router is not None,
+            "shared_expert": ("folded" if layer.folded else "separate") if shape.shared_intermediate else None,
             "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
         "roofline": {

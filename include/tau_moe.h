@@ -125,7 +125,9 @@ int tau_launch_fused_bf16_moe_decode(const void* input, const void* logits, cons
                                      const TauDecodeProfile* gate_up_config, const TauDecodeProfile* down_config,
                                      int* receipts, void* stream);
 
-/* ---------------- generalised entry points (any E <= 512, K <= 32) ---------------- */
+/* ---------------- generalised entry points (any E <= 512, K <= 32; the layer
+ * entry points take E + 1 <= 513 experts from given routes when a shared expert
+ * is folded in) ---------------- */
 
 /* Capacity of the padded dispatch, generalising moe_prefill_capacity_for_tile
  * (crates/cuda-kernels/src/moe/prefill.rs:17-30); -1 for invalid input. */
@@ -233,6 +235,27 @@ int tau_launch_centered_rms_norm(const void* input, const void* weight, void* ou
  * from those logits.  Two launches (projection with the bias fused; routing). */
 int tau_launch_moe_router_route_ex(const void* input, const void* weight, const float* bias, float* logits,
                                    float* routes, int tokens, int hidden, int experts, int top_k, void* stream);
+
+/* The always-on shared expert folded into the routed schedule (the
+ * shared-expert branch of SparseMoeBlock::forward_routed, sparse_moe.rs:102-151,
+ * and SharedExpert::combine, shared_expert.rs:39-69, run as one more expert):
+ * logits f32/BF16 [T, E+1] hold the E router logits then the shared gate logit
+ * x . w_s; routes [T, 2(K+1)] get the routed top-K at ranks 0..K-1 exactly as
+ * tau_launch_moe_routing_ex writes them and (id E, weight sigmoid(gate)) at
+ * rank K.  With expert E's weights appended to the banks (gate_up
+ * [E+1, 2I, H], down [E+1, H, I]; requires the shared intermediate size = I),
+ * tau_launch_moe_prefill_ex(logits = NULL, experts = E+1, top_k = K+1)
+ * computes routed + sigmoid(x . w_s) * shared(x) in one grouped schedule
+ * (contributions summed in f32 in rank order, rounded once). */
+int tau_launch_moe_routing_shared_ex(const void* logits, int logits_dtype, float* routes, int tokens, int experts,
+                                     int top_k, void* stream);
+
+/* The same from hidden states: weight BF16 [E+1, H] = router rows then w_s,
+ * bias f32 [E+1] (may be NULL; the shared gate has none, so bias[E] = 0),
+ * logits f32 [T, E+1] (required), then the routing above. */
+int tau_launch_moe_router_route_shared_ex(const void* input, const void* weight, const float* bias, float* logits,
+                                          float* routes, int tokens, int hidden, int experts, int top_k,
+                                          void* stream);
 
 /* Load-time weight preparation (no reference counterpart: the reference's
  * kernels read its packed [E, n, k] storage directly, sparse_moe/experts.rs:

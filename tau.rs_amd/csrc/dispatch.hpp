@@ -87,11 +87,13 @@ __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p, size_t 
 // and, when `eids` is non-null, the K selected experts (or -1 for every rank
 // of a rejected row) at eids[0..K).  Returns true when the row was rejected.
 // Rows with `active == false` take part in the DPP steps but write nothing.
+// Layout overrides (0 = default): `ldl` logits per row (E), `routes_stride`
+// floats per routes row (2K) and `weights_ofs` offset of the weights in it (K).
 template <int EP, typename T>
 __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, float* routes, int E, int K,
-                                          int* eids) {
+                                          int* eids, int ldl = 0, int routes_stride = 0, int weights_ofs = 0) {
     const int l16 = threadIdx.x & 15;
-    const T* row = logits + (size_t)(active ? t : 0) * E;
+    const T* row = logits + (size_t)(active ? t : 0) * (ldl ? ldl : E);
     float d[EP], p[EP];  // p: exp(x - max) numerators
     uint32_t nonfinite = 0;
     float maximum = -INFINITY;
@@ -225,13 +227,14 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
         for (int r = 0; r < K; ++r) publish(r, pick());
     }
     if (active) {
-        float* out = routes + (size_t)t * 2 * K;
+        float* out = routes + (size_t)t * (routes_stride ? routes_stride : 2 * K);
+        const int wofs = weights_ofs ? weights_ofs : K;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int rank = s * 16 + l16;
             if (rank < K) {
                 out[rank] = nonfinite ? __builtin_nanf("") : (float)my_id[s];
-                out[K + rank] = nonfinite ? __builtin_nanf("") : my_p[s] / selected_sum;
+                out[wofs + rank] = nonfinite ? __builtin_nanf("") : my_p[s] / selected_sum;
                 if (eids) eids[rank] = nonfinite ? -1 : my_id[s];
             }
         }
@@ -245,6 +248,25 @@ template <int EP, typename T>
 __global__ __launch_bounds__(64) void route_kernel(const T* logits, float* routes, int T_, int E, int K) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
     route_row<EP, T>(logits, t, t < T_, routes, E, K, nullptr);
+}
+
+// Routing with an always-on shared expert folded in as expert E: logits rows
+// hold E router logits then the shared gate logit x . w_s; ranks 0..K-1 are
+// the routed top-K as route_kernel writes them, rank K is (id E, weight
+// sigmoid(gate)), in rows of 2(K+1) floats.  A rejected routed row (or a
+// non-finite gate, through its weight) invalidates the plan as before.
+template <int EP, typename T>
+__global__ __launch_bounds__(64) void route_shared_kernel(const T* logits, float* routes, int T_, int E, int K) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
+    const bool active = t < T_;
+    const int K1 = K + 1;
+    const bool bad = route_row<EP, T>(logits, t, active, routes, E, K, nullptr, E + 1, 2 * K1, K1);
+    if (active && (threadIdx.x & 15) == 0) {
+        const float gate = load_logit<T>(logits, (size_t)t * (E + 1) + E);
+        float* out = routes + (size_t)t * 2 * K1;
+        out[K] = bad ? __builtin_nanf("") : (float)E;
+        out[K1 + K] = bad ? __builtin_nanf("") : sigmoid(gate);
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -39,6 +39,8 @@ int launch_add_bias(float* out, const float* bias, int rows, int cols, hipStream
 bool gemm_rows_supported(int bm);
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);
+int launch_routing_shared(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
+                          hipStream_t s);
 int launch_routing(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                    hipStream_t s);
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,

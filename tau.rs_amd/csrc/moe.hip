@@ -92,9 +92,13 @@ GemmArgs down_args(const void* activated, const void* down, const float* routes,
     return g;
 }
 
+// Up to 512 routed experts, plus one when a shared expert is folded in as
+// expert E (its routes come from tau_launch_moe_routing_shared_ex).
+constexpr int kMaxLayerExperts = 513;
+
 bool shape_ok(int tokens, int hidden, int intermediate, int experts, int top_k) {
     return tokens > 0 && tokens <= kMaxTokens && hidden > 0 && intermediate > 0 && intermediate <= INT_MAX / 2 &&
-           experts > 0 && experts <= 512 && top_k > 0 && top_k <= 32 && top_k <= experts &&
+           experts > 0 && experts <= kMaxLayerExperts && top_k > 0 && top_k <= 32 && top_k <= experts &&
            (int64_t)tokens * top_k * hidden <= (int64_t)1 << 40;
 }
 
@@ -117,10 +121,26 @@ int tau_launch_moe_router_route_ex(const void* input, const void* weight, const 
     return launch_routing(logits, 0, routes, tokens, experts, top_k, as_stream(stream));
 }
 
+int tau_launch_moe_routing_shared_ex(const void* logits, int logits_dtype, float* routes, int tokens, int experts,
+                                     int top_k, void* stream) {
+    if (tokens <= 0 || tokens > kMaxTokens) return kInvalid;
+    return launch_routing_shared(logits, logits_dtype, routes, tokens, experts, top_k, as_stream(stream));
+}
+
+int tau_launch_moe_router_route_shared_ex(const void* input, const void* weight, const float* bias, float* logits,
+                                          float* routes, int tokens, int hidden, int experts, int top_k,
+                                          void* stream) {
+    if (!routes || experts <= 0 || experts > 512 || top_k <= 0 || top_k + 1 > 32 || top_k > experts)
+        return kInvalid;
+    const int code = tau_launch_moe_router_ex(input, weight, bias, logits, tokens, hidden, experts + 1, stream);
+    if (code) return code;
+    return launch_routing_shared(logits, 0, routes, tokens, experts, top_k, as_stream(stream));
+}
+
 int tau_launch_moe_router_ex(const void* input, const void* weight, const float* bias, float* logits, int tokens,
                              int hidden, int experts, void* stream) {
     if (!input || !weight || !logits || tokens <= 0 || tokens > kMaxTokens || hidden <= 0 || experts <= 0 ||
-        experts > 512)
+        experts > kMaxLayerExperts)
         return kInvalid;
     if (router_logits_supported(input, weight, hidden, experts))  // skinny-GEMM kernel, bias fused
         return launch_router_logits(input, weight, bias, logits, tokens, hidden, experts, as_stream(stream));
@@ -247,7 +267,8 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
                               int weight_layout, const void* residual, int* receipts, void* stream) {
     if (!input || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
         !contributions || !output || !shape_ok(tokens, hidden, intermediate, experts, top_k) ||
-        !layout_ok(weight_layout, hidden, intermediate) || (logits && logits_dtype != 0 && logits_dtype != 1) ||
+        !layout_ok(weight_layout, hidden, intermediate) ||
+        (logits && ((logits_dtype != 0 && logits_dtype != 1) || experts > 512)) ||
         !gemm_rows_supported(tile_rows) || capacity < capacity_for(tokens, experts, top_k, tile_rows) ||
         capacity % tile_rows)
         return kInvalid;

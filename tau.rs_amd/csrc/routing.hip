@@ -75,7 +75,7 @@ struct HistLaunch {
 
 // Largest expert count the routing/dispatch kernels accept (32 logits per
 // lane of a 16-lane row; dispatch LDS (19 E + 5122) words, 59 KB at E = 512).
-constexpr int kMaxExperts = 512;
+constexpr int kMaxExperts = 512;  // routed experts (16 lanes x 32 logits per token row)
 constexpr int kMaxTopK = 32;
 
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M) {
@@ -94,13 +94,43 @@ int launch_routing(const void* logits, int logits_dtype, float* routes, int toke
     return launch_route<float>((const float*)logits, routes, tokens, E, K, s);
 }
 
+namespace {
+
+template <typename T>
+int launch_route_shared(const T* logits, float* routes, int tokens, int E, int K, hipStream_t s) {
+    const int blocks = (tokens + 3) / 4;
+    const int ep = (E + 15) / 16;
+    if (ep <= 1) route_shared_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 2) route_shared_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 4) route_shared_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 8) route_shared_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else if (ep <= 16) route_shared_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    else route_shared_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// Routing with the shared expert folded in (route_shared_kernel): logits
+// [T, E+1], routes [T, 2(K+1)].
+int launch_routing_shared(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
+                          hipStream_t s) {
+    if (!logits || !routes || tokens <= 0 || E <= 0 || E > kMaxExperts || K <= 0 || K > E || K + 1 > kMaxTopK ||
+        (logits_dtype != 0 && logits_dtype != 1))
+        return kInvalid;
+    if (logits_dtype == 1) return launch_route_shared<uint16_t>((const uint16_t*)logits, routes, tokens, E, K, s);
+    return launch_route_shared<float>((const float*)logits, routes, tokens, E, K, s);
+}
+
 // Dispatch; with logits, routing runs inside the plan kernels.  `scratch`
 // (optional) enables the multi-workgroup plan for large batches.
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,
                     int* tiles, int tokens, int E, int K, int M, int capacity, void* scratch, size_t scratch_bytes,
                     hipStream_t s) {
-    if (!routes || !meta || !offsets || !slots || !tiles || tokens <= 0 || E <= 0 || E > kMaxExperts || K <= 0 ||
-        K > E || K > kMaxTopK || M <= 0 || capacity <= 0 || capacity % M)
+    // From given routes one more expert is allowed: a shared expert folded in as expert E.
+    if (!routes || !meta || !offsets || !slots || !tiles || tokens <= 0 || E <= 0 ||
+        E > kMaxExperts + (logits ? 0 : 1) || K <= 0 || K > E || K > kMaxTopK || M <= 0 || capacity <= 0 ||
+        capacity % M)
         return kInvalid;
     if ((int64_t)tokens * K > (int64_t)1 << 30) return kInvalid;
     if ((int64_t)capacity < capacity_for(tokens, E, K, M)) return kInvalid;

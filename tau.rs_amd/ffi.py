@@ -40,6 +40,8 @@ EXPORTS = (
     "tau_moe_pack_weights",
     "tau_launch_moe_router_ex",
     "tau_launch_moe_router_route_ex",
+    "tau_launch_moe_routing_shared_ex",
+    "tau_launch_moe_router_route_shared_ex",
     "tau_launch_fused_residual_rms_norm",
     "tau_launch_centered_rms_norm_configured",
     "tau_launch_centered_rms_norm",
@@ -104,6 +106,8 @@ def lib():
         "tau_moe_pack_weights": [p, p, i, i, i, p],
         "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
         "tau_launch_moe_router_route_ex": [p, p, p, p, p, i, i, i, i, p],
+        "tau_launch_moe_routing_shared_ex": [p, i, p, i, i, i, p],
+        "tau_launch_moe_router_route_shared_ex": [p, p, p, p, p, i, i, i, i, p],
         "tau_launch_fused_residual_rms_norm": [p, p, p, p, p, i, i, f32, i, p, i],
         "tau_launch_centered_rms_norm_configured": [p, p, p, i, i, f32, i, p, i],
         "tau_launch_centered_rms_norm": [p, p, p, i, i, f32, i, p],
@@ -232,6 +236,21 @@ def router_route_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.T
     e = weight.shape[0]
     check(lib().tau_launch_moe_router_route_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(routes), t, h, e,
                                                top_k, stream_ptr(stream)), "MoE router + routing")
+
+
+def routing_shared_ex(logits, routes, experts, top_k, stream=None):
+    """routes [T, 2(K+1)] from logits [T, E+1]: routed top-K, then (E, sigmoid(gate))."""
+    t = logits.shape[0]
+    check(lib().tau_launch_moe_routing_shared_ex(ptr(logits), _dtype_code(logits), ptr(routes), t, experts, top_k,
+                                                 stream_ptr(stream)), "MoE routing with shared expert")
+
+
+def router_route_shared_ex(x, weight, bias, logits, routes, experts, top_k, stream=None):
+    """logits f32 [T, E+1] and routes [T, 2(K+1)] from x BF16 [T, H]; weight [E+1, H]."""
+    t, h = x.shape
+    check(lib().tau_launch_moe_router_route_shared_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(routes), t, h,
+                                                      experts, top_k, stream_ptr(stream)),
+          "MoE router + routing with shared expert")
 
 
 def router_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor, stream=None):

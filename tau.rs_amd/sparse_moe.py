@@ -119,8 +119,14 @@ class MoePrefillRunner:
     "row_major" / "frag16" force one layout."""
 
     def __init__(self, config: SparseMoeConfig, gate_up: torch.Tensor, down: torch.Tensor,
-                 tile_rows: Optional[int] = None, weight_layout: str = "auto"):
+                 tile_rows: Optional[int] = None, weight_layout: str = "auto", fold_shared: bool = False):
+        """fold_shared: the banks hold one more expert, the shared expert, which
+        every token takes at rank K (routes from tau_launch_moe_routing_shared_ex);
+        the runner then launches E+1 experts and K+1 picks."""
         config.validate()
+        if fold_shared:
+            config = dataclasses.replace(config, num_experts=config.num_experts + 1,
+                                         experts_per_token=config.experts_per_token + 1, shared_expert=None)
         E, I, H = config.num_experts, config.expert_intermediate_size, config.hidden_size
         if gate_up.shape != (E, 2 * I, H) or down.shape != (E, H, I):
             raise ValueError("packed expert weights must be gate_up [E,2I,H] and down [E,H,I]")
@@ -193,14 +199,15 @@ class MoePrefillRunner:
                 stream=None, residual: Optional[torch.Tensor] = None, router=None) -> torch.Tensor:
         """Routed-expert output; with `residual` (BF16 [T, H]) returns
         bf16(output + residual), the layer's residual add fused in the combine.
-        logits None: `router` = (weight BF16 [E,H], bias f32 [E] or None,
-        logits_out f32 [T,E] or None) and the router projection runs fused
-        with the routing (tau_launch_moe_router_route_ex)."""
+        logits None: `router(routes)` writes the [T, 2K] routes into the
+        workspace's routes buffer (the router projection with the routing,
+        tau_launch_moe_router_route_ex, or the shared-expert routing) and the
+        layer starts from them."""
         c = self.config
         if x.dim() != 2 or x.shape[1] != c.hidden_size or x.dtype != torch.bfloat16:
             raise ValueError("input must be BF16 [tokens, hidden]")
         if logits is None and router is None:
-            raise ValueError("pass router logits or the router weights")
+            raise ValueError("pass router logits or a routes producer")
         if logits is not None and logits.shape != (x.shape[0], c.num_experts):
             raise ValueError("router logits must be [tokens, num_experts]")
         tokens = x.shape[0]
@@ -211,8 +218,7 @@ class MoePrefillRunner:
             out = torch.empty_like(x)
         x = x.contiguous()
         if logits is None:
-            w, b, logits_out = router
-            ffi.router_route_ex(x, w, b, logits_out, ws["routes"], c.experts_per_token, stream=stream)
+            router(ws["routes"])
         else:
             logits = logits.contiguous()
         ffi.prefill_ex(x, logits, self.gate_up, self.down, ws, out, c.num_experts,
@@ -244,24 +250,49 @@ class SparseMoeBlock:
 
     def __init__(self, config: SparseMoeConfig, gate_up, down, shared_gate_up=None, shared_down=None,
                  shared_gate=None, tile_rows: Optional[int] = None, weight_layout: str = "auto",
-                 router_weight: Optional[torch.Tensor] = None, router_bias: Optional[torch.Tensor] = None):
-        self.runner = MoePrefillRunner(config, gate_up, down, tile_rows, weight_layout)
+                 router_weight: Optional[torch.Tensor] = None, router_bias: Optional[torch.Tensor] = None,
+                 fold_shared: Optional[bool] = None):
+        config.validate()
+        E, H, I, K = config.num_experts, config.hidden_size, config.expert_intermediate_size, config.experts_per_token
+        se = config.shared_expert
+        if se is not None:
+            if shared_gate_up is None or shared_down is None:
+                raise ValueError("shared expert weights missing")
+            if se.gated and shared_gate is None:
+                raise ValueError("shared expert gate weight missing")
+        # A gated shared expert with the experts' intermediate size runs as
+        # expert E of the routed schedule (default when possible).
+        foldable = (se is not None and se.gated and se.intermediate_size == I and K + 1 <= 32
+                    and tuple(shared_gate_up.shape) == (2 * I, H) and tuple(shared_down.shape) == (H, I))
+        self.folded = foldable if fold_shared is None else bool(fold_shared)
+        if self.folded and not foldable:
+            raise ValueError("folding needs a gated shared expert with the experts' intermediate size and K < 32")
+        if self.folded:
+            gu_all = torch.cat([gate_up, shared_gate_up.unsqueeze(0).to(gate_up.dtype)], 0)
+            dn_all = torch.cat([down, shared_down.unsqueeze(0).to(down.dtype)], 0)
+            self.runner = MoePrefillRunner(config, gu_all, dn_all, tile_rows, weight_layout, fold_shared=True)
+            del gu_all, dn_all
+        else:
+            self.runner = MoePrefillRunner(config, gate_up, down, tile_rows, weight_layout)
         self.config = config
         self.router = None
         if router_weight is not None:
-            E, H = config.num_experts, config.hidden_size
             if router_weight.shape != (E, H) or router_weight.dtype != torch.bfloat16:
                 raise ValueError("router weight must be BF16 [num_experts, hidden]")
             if router_bias is not None and (router_bias.shape != (E,) or router_bias.dtype != torch.float32):
                 raise ValueError("router bias must be f32 [num_experts]")
-            self.router = (router_weight.contiguous(), None if router_bias is None else router_bias.contiguous())
+            w, b = router_weight.contiguous(), None if router_bias is None else router_bias.contiguous()
+            if self.folded:  # the shared gate row w_s after the router rows, no bias for it
+                w = torch.cat([w, shared_gate.reshape(1, H).to(torch.bfloat16)], 0).contiguous()
+                if b is not None:
+                    b = torch.cat([b, torch.zeros(1, dtype=b.dtype, device=b.device)]).contiguous()
+            self.router = (w, b)
         self._logits = None
+        self._gate_logits = None
         self.shared = None
-        if config.shared_expert is not None:
-            if shared_gate_up is None or shared_down is None:
-                raise ValueError("shared expert weights missing")
-            if config.shared_expert.gated and shared_gate is None:
-                raise ValueError("shared expert gate weight missing")
+        if self.folded:
+            self.shared_gate = shared_gate.reshape(1, H).to(torch.bfloat16).contiguous()
+        elif se is not None:
             gu, dn = shared_gate_up.contiguous(), shared_down.contiguous()
             Is, H = config.shared_expert.intermediate_size, config.hidden_size
             self.shared_layout = ffi.WEIGHTS_ROW_MAJOR
@@ -272,25 +303,48 @@ class SparseMoeBlock:
         self._shared_ws = None
 
     def logits(self, x: torch.Tensor, stream=None) -> torch.Tensor:
-        """Router scores f32 [T, E] (x . W_r^T + b)."""
+        """Router scores f32 [T, E] (x . W_r^T + b); with the shared expert
+        folded in, [T, E+1] with the gate logit x . w_s last."""
         if self.router is None:
             raise ValueError("block built without router weights: pass logits to forward")
-        T, E = x.shape[0], self.config.num_experts
-        if self._logits is None or self._logits.shape[0] < T:
-            self._logits = torch.empty(_next_pow2(T), E, dtype=torch.float32, device=x.device)
-        out = self._logits[:T]
+        out = self._logits_buffer(x.shape[0], x.device)
         ffi.router_ex(x, self.router[0], self.router[1], out, stream=stream)
         return out
 
-    def _fused_router(self, x: torch.Tensor):
-        """(weight, bias, logits_out) for the router + routing call, or None
-        without router weights."""
+    def _logits_buffer(self, T: int, device):
+        E = self.config.num_experts + (1 if self.folded else 0)
+        if self._logits is None or self._logits.shape[0] < T:
+            self._logits = torch.empty(_next_pow2(T), E, dtype=torch.float32, device=device)
+        return self._logits[:T]
+
+    def _fused_router(self, x: torch.Tensor, stream=None):
+        """routes(routes_buffer) for the router + routing call (with the shared
+        expert's gate when folded), or None without router weights."""
         if self.router is None:
             return None
-        T, E = x.shape[0], self.config.num_experts
-        if self._logits is None or self._logits.shape[0] < T:
-            self._logits = torch.empty(_next_pow2(T), E, dtype=torch.float32, device=x.device)
-        return self.router[0], self.router[1], self._logits[:T]
+        w, b = self.router
+        logits = self._logits_buffer(x.shape[0], x.device)
+        E, K = self.config.num_experts, self.config.experts_per_token
+        if self.folded:
+            return lambda routes: ffi.router_route_shared_ex(x, w, b, logits, routes, E, K, stream=stream)
+        return lambda routes: ffi.router_route_ex(x, w, b, logits, routes, K, stream=stream)
+
+    def _shared_routes(self, x: torch.Tensor, logits: torch.Tensor, stream=None):
+        """routes(routes_buffer) from caller logits for the folded shared expert:
+        [T, E+1] as given, or [T, E] plus the gate column x . w_s projected here."""
+        E, K = self.config.num_experts, self.config.experts_per_token
+        T = x.shape[0]
+        if logits.shape == (T, E + 1):
+            ext = logits.contiguous()
+        elif logits.shape == (T, E):
+            if self._gate_logits is None or self._gate_logits.shape[0] < T:
+                self._gate_logits = torch.empty(_next_pow2(T), 1, dtype=torch.float32, device=x.device)
+            gate = self._gate_logits[:T]
+            ffi.router_ex(x, self.shared_gate, None, gate, stream=stream)
+            ext = torch.cat([logits.float(), gate], 1) if logits.dtype != torch.float32 else torch.cat([logits, gate], 1)
+        else:
+            raise ValueError("router logits must be [tokens, num_experts] (or + 1 shared gate column)")
+        return lambda routes: ffi.routing_shared_ex(ext, routes, E, K, stream=stream)
 
     def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None,
                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -300,14 +354,16 @@ class SparseMoeBlock:
         (tau_launch_moe_router_route_ex; the projection is kept in the block's
         logits buffer) and the layer starts from those routes."""
         router = None
+        x = x.contiguous()
         if logits is None:
-            x = x.contiguous()
-            router = self._fused_router(x)
+            router = self._fused_router(x, stream=stream)
             if router is None:
                 raise ValueError("block built without router weights: pass logits to forward")
+        elif self.folded:
+            router, logits = self._shared_routes(x, logits, stream=stream), None
         if residual is not None and (residual.shape != x.shape or residual.dtype != torch.bfloat16):
             raise ValueError("residual must be BF16 shaped like the input")
-        if self.shared is None:
+        if self.shared is None:  # no shared expert, or folded into the routed schedule
             return self.runner.forward(x, logits, stream=stream, residual=residual, router=router)
         routed = self.runner.forward(x, logits, stream=stream, router=router)
         gu, dn, gw = self.shared

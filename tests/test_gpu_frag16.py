@@ -89,16 +89,17 @@ def test_frag16_grouped_projection_bit_identical(tau, projection):
         np.testing.assert_array_equal(bits(o1), bits(o2))
 
 
-def test_frag16_shared_expert_bit_identical(tau):
+@pytest.mark.parametrize("fold", [False, True])
+def test_frag16_shared_expert_bit_identical(tau, fold):
     shape = tau.inputs.scaled(tau.inputs.CONFIGS["c4_next_sparse"], 96)
-    say(f"[frag16 shared expert] T={shape.tokens}")
+    say(f"[frag16 shared expert] T={shape.tokens} folded={fold}")
     layer = tau.inputs.make_layer(shape)
     cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k,
                               shared_expert=tau.SharedExpertConfig(shape.shared_intermediate, gated=True))
     outs = []
     for lay in ("row_major", "frag16"):
         blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer["shared_gate_up"],
-                                 layer["shared_down"], layer["shared_gate"], weight_layout=lay)
+                                 layer["shared_down"], layer["shared_gate"], weight_layout=lay, fold_shared=fold)
         outs.append(blk.forward(layer["x"], layer["logits"]))
         torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(outs[0]), bits(outs[1]))

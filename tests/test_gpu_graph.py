@@ -14,18 +14,20 @@ def bits(t):
     return t.view(torch.int16).cpu().numpy()
 
 
-@pytest.mark.parametrize("which", ["c2", "c3_t256", "c4_t96"])
+@pytest.mark.parametrize("which", ["c2", "c3_t256", "c4_t96", "c4_t96_apart"])
 def test_graph_replays_equal_eager(tau, which):
     C = tau.inputs.CONFIGS
     shape = {"c2": C["c2_30b_a3b_decode"], "c3_t256": tau.inputs.scaled(C["c3_30b_a3b_prefill"], 256),
-             "c4_t96": tau.inputs.scaled(C["c4_next_sparse"], 96)}[which]
+             "c4_t96": tau.inputs.scaled(C["c4_next_sparse"], 96),
+             "c4_t96_apart": tau.inputs.scaled(C["c4_next_sparse"], 96)}[which]
     print(f"[graph] {shape.name}", flush=True)
     layer = tau.inputs.make_layer(shape)
     shared = tau.SharedExpertConfig(shape.shared_intermediate) if shape.shared_intermediate else None
     cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k, shared_expert=shared)
     blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer.get("shared_gate_up"),
                              layer.get("shared_down"), layer.get("shared_gate"),
-                             router_weight=layer["router"].to(torch.bfloat16), router_bias=layer["bias"])
+                             router_weight=layer["router"].to(torch.bfloat16), router_bias=layer["bias"],
+                             fold_shared=False if which.endswith("apart") else None)
     x = layer["x"].clone()
     res = torch.zeros_like(x) if shared is not None else None
     graph, out = blk.capture(x, None, residual=res)

@@ -402,7 +402,7 @@ def test_shared_expert_path_matches_oracle(tau, oracle, tokens):
     cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k,
                               shared_expert=tau.SharedExpertConfig(shape.shared_intermediate))
     block = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer["shared_gate_up"], layer["shared_down"],
-                               layer["shared_gate"])
+                               layer["shared_gate"], fold_shared=False)  # the reference's separate shared combine
     out = block.forward(layer["x"], layer["logits"])
     torch.cuda.synchronize()
     x = f32(layer["x"])
