@@ -301,12 +301,12 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
     d.receipt = receipts ? receipts + 5 : nullptr;
 
     // Column blocks per wave and K batch depth measured on MI355X for these
-    // kernels (frag16 gate_up 2 x 16 columns, 4 x 32 K; down 4 x 16 columns,
+    // kernels (frag16 gate_up 2 x 16 columns, 8 x 32 K; down 4 x 16 columns,
     // 4 x 32 K for K < 1024 (Qwen3-30B-A3B), 2 x 16 columns, 8 x 32 K for
     // longer rows (Qwen3-235B-A22B)); the plan workgroup of the down launch
     // has the same 256 threads as the GEMM workgroups.
     if (weight_layout == kWeightsFrag16) {
-        code = launch_decode_gemm<kEpiSilu, 2, 4, 4, kWeightsFrag16, false>(g, plan, 0, s);
+        code = launch_decode_gemm<kEpiSilu, 2, 8, 4, kWeightsFrag16, false>(g, plan, 0, s);
         if (code) return code;
         if (intermediate < 1024)
             code = launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);

@@ -942,10 +942,10 @@ template <int AM, int EPI, int RT, int WL>
 int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
     // Row-major weights: SiLU streams two weight rows per column and prefers
     // one 16-column block per wave; single-stream projections prefer four.
-    // Frag16 weights (1 KB contiguous fragments): two blocks per wave, with
-    // deeper K batches for the single-stream projections.
+    // Frag16 weights (1 KB contiguous fragments): two blocks per wave, eight
+    // K steps per batch.
     constexpr int NB = WL == kWeightsFrag16 ? 2 : (EPI == kEpiSilu ? 1 : 4);
-    constexpr int U = WL == kWeightsFrag16 && EPI != kEpiSilu ? 8 : 4;
+    constexpr int U = WL == kWeightsFrag16 ? 8 : 4;
     const int rows = 16 * RT;
     const long m_blocks = (p.rows + rows - 1) / rows;
     if (!aligned) {
