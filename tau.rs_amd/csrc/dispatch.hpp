@@ -275,7 +275,6 @@ __global__ __launch_bounds__(64) void route_shared_kernel(const T* logits, float
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSpanLds = 4096;      // assignments whose experts fit the LDS stage
-constexpr int kPlanLdsWords = 4096; // bound on [chunks][E] counts each chunk workgroup sums
 constexpr int kSplitRouteTokens = 32;  // batches from this size route in their own launch
 
 // Validates one externally supplied assignment (moe_dispatch.cu:23-33 of the

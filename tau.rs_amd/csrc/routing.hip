@@ -152,11 +152,11 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
     while ((1 << bits) < E) ++bits;
     a.expert_bits = bits;
     const size_t lds = sizeof(int) * dispatch_lds_words(E);
-    // Multi-workgroup chunks: as many as the plan workgroup can stage
-    // ([chunks][E] counts in LDS, at most 64), each a whole number of 64-token
+    // Multi-workgroup chunks: at most 64 (each scatter workgroup sums the
+    // [chunks][E] counts from scratch), each a whole number of 64-token
     // routing passes that fits the LDS expert stage.
     {
-        const int max_chunks = std::max(1, std::min(64, kPlanLdsWords / E));
+        const int max_chunks = 64;
         const int stage_tokens = std::max(1, kSpanLds / K);
         int ct = (tokens + max_chunks - 1) / max_chunks;
         ct = (ct + 63) / 64 * 64;
@@ -164,8 +164,7 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
         a.chunk_tokens = ct;
     }
     const int chunks = (tokens + a.chunk_tokens - 1) / a.chunk_tokens;
-    const bool multi = chunks > 1 && scratch && (size_t)chunks * E <= (size_t)kPlanLdsWords &&
-                       scratch_bytes >= sizeof(int) * ((size_t)chunks * E + chunks);
+    const bool multi = chunks > 1 && scratch && scratch_bytes >= sizeof(int) * ((size_t)chunks * E + chunks);
     if (!multi) {
         // Route separately (every CU) unless the batch is a few tokens, whose
         // routing the plan workgroup does faster than an extra launch.
