@@ -178,3 +178,37 @@ def test_routing_wide_top_k_with_ties(tau, oracle, case):
     np.testing.assert_array_equal(meta.cpu().numpy(), m_ref)
     np.testing.assert_array_equal(slots.cpu().numpy(), s_ref)
     np.testing.assert_array_equal(tiles.cpu().numpy(), t_ref)
+
+
+def test_c1_f32_config_routing_and_layer(tau, oracle):
+    """Config 0 (f32, H=256, E=8, K=2, I=512, 16 tokens,
+    seed 0): the f32 router logits route on the GPU exactly as the oracle's f32
+    CPU plan, with the smallest K-th / (K+1)-th logit gap reported (distinct
+    f32 logits cannot produce equal probabilities unless that gap is ~1 ulp);
+    the layer on BF16 copies of the f32 inputs stays within the north-star
+    tolerance of the f32 path on the f32 originals."""
+    shape = tau.inputs.CONFIGS["c1_tiny_f32"]
+    layer = tau.inputs.make_layer(shape)
+    T, E, K = shape.tokens, shape.experts, shape.top_k
+    logits = layer["logits"].float().contiguous()
+    lg = to_np(logits)
+    srt = -np.sort(-lg, axis=1)
+    gap = float(np.min(srt[:, K - 1] - srt[:, K]))
+    say(f"[c1 f32] smallest K-th/(K+1)-th logit gap {gap:.3e}")
+    assert gap > 0.0
+    routes = torch.empty(T, 2 * K, dtype=torch.float32, device="cuda")
+    tau.ffi.routing_ex(logits, routes, E, K)
+    torch.cuda.synchronize()
+    ids, w = oracle.route(lg, K)
+    r = to_np(routes)
+    np.testing.assert_array_equal(r[:, :K].astype(np.int64), ids)
+    assert np.all(np.abs(r[:, K:] - w) <= 1e-7 + 1e-5 * np.abs(w))
+    bf = {k: layer[k].to(torch.bfloat16) for k in ("x", "gate_up", "down")}
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, E, K)
+    runner = tau.MoePrefillRunner(cfg, bf["gate_up"], bf["down"])
+    out = runner.forward(bf["x"], logits)
+    torch.cuda.synchronize()
+    ref = oracle.moe(to_np(layer["x"]), ids, w, to_np(layer["gate_up"]), to_np(layer["down"]))
+    e = rel_l2(to_np(out), ref)
+    say(f"    rel_l2 vs f32 path on the f32 inputs {e:.2e}")
+    assert e <= 1e-2
