@@ -349,6 +349,8 @@ def main():
                          "projection_us": time_events(torch, layer.project_router, n_proj) * 1e3}
     dominant = "gate_up" if ms_gu >= ms_dn else "down"
     achieved = gu_rate if dominant == "gate_up" else dn_rate
+    ms_dom = ms_gu if dominant == "gate_up" else ms_dn
+    traffic = measured_traffic(shape.name, dominant, layout_name)
 
     tokens_per_s = T / (ms_step * 1e-3)
     layer_hbm = bytes_ / (ms_step * 1e-3) / 1e9
@@ -377,7 +379,10 @@ def main():
         },
         "roofline": {
             "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": measured_traffic(shape.name, dominant, layout_name),
+            "frac": achieved / peak, "traffic": traffic,
+            # the same kernel against HBM, from its measured bytes (rocprofv3 FETCH/WRITE_SIZE)
+            "traffic_GBs": traffic / (ms_dom * 1e-3) / 1e9 if traffic else None,
+            "traffic_hbm_frac": traffic / (ms_dom * 1e-3) / 1e9 / HBM_PEAK_GBS if traffic else None,
             "kernel_ms": {"gate_up": ms_gu, "down": ms_dn},
             "algorithmic_per_launch": {"gate_up": traffic_alg[0], "down": traffic_alg[1]},
         },
