@@ -350,12 +350,12 @@ def main():
     dominant = "gate_up" if ms_gu >= ms_dn else "down"
     achieved = gu_rate if dominant == "gate_up" else dn_rate
     ms_dom = ms_gu if dominant == "gate_up" else ms_dn
+    layout_name = "frag16" if layer.layout == tau.ffi.WEIGHTS_FRAG16 else "row_major"
     traffic = measured_traffic(shape.name, dominant, layout_name)
 
     tokens_per_s = T / (ms_step * 1e-3)
     layer_hbm = bytes_ / (ms_step * 1e-3) / 1e9
     layer_mfma = flops / (ms_step * 1e-3) / 1e12
-    layout_name = "frag16" if layer.layout == tau.ffi.WEIGHTS_FRAG16 else "row_major"
     result = {
         "metric": "MoE-layer tokens/s; % bf16 MFMA peak (prefill), % HBM BW (decode)",
         "value": tokens_per_s,
