@@ -227,7 +227,7 @@ def cpu_baseline(layer, seconds):
     oracle.set_threads(threads)
     times = []
     t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 25):
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 2000):  # ~`seconds` of CPU work
         t0 = time.perf_counter()
         ids, w = oracle.route(lg, s.top_k)
         routed = oracle.moe(x, ids, w, gu, dn)
