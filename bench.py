@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--banks", type=int, default=0, help="weight banks to rotate (0 = auto)")
     ap.add_argument("--tile-rows", type=int, default=0, help="override the library's row-block choice")
+    ap.add_argument("--tokens", type=int, default=0, help="run the workload's layer at this many tokens")
     ap.add_argument("--weight-layout", choices=("auto", "row_major", "frag16"), default="auto",
                     help="expert weight layout held by the runner (auto: FRAG16 when the shape allows)")
     ap.add_argument("--with-norm", action="store_true",
@@ -288,6 +289,8 @@ def main():
         return
     tau = load_package()
     shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
+    if args.tokens:
+        shape = tau.inputs.scaled(shape, args.tokens)
     weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
     banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
     layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm, args.with_router,

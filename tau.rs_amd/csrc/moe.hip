@@ -170,11 +170,15 @@ int tau_moe_select_tile_rows(int tokens, int experts, int top_k, int hidden, int
     (void)intermediate;
     if (tokens <= 0 || experts <= 0 || top_k <= 0) return 16;
     const double rows_per_expert = (double)tokens * top_k / experts;
-    // Decode-sized groups stream weights; anything larger uses 256-row MFMA
-    // tiles, whose all-padding wave rows skip their MFMAs, so skewed routing
-    // (few hot experts) and balanced routing both keep the weight panels in
-    // as few tiles as possible.
-    if (rows_per_expert <= 16.0) return 16;
+    // Measured on MI355X over balanced (30B-A3B, 235B-A22B) and skewed (biased,
+    // Zipf) routing, 128..8192 tokens: decode batches (<= 64 tokens, the fused
+    // decode path) and <= 8 rows per expert stream weights in 16-row groups;
+    // <= 16 rows, 32-row groups; <= 32 rows, 128-row MFMA tiles; beyond, 256-row
+    // MFMA tiles (whose all-padding wave rows skip their MFMAs), which skewed
+    // routing prefers from ~32 rows per expert on.
+    if (tokens <= 64 || rows_per_expert <= 8.0) return 16;
+    if (rows_per_expert <= 16.0) return 32;
+    if (rows_per_expert <= 32.0) return 128;
     return 256;
 }
 
