@@ -634,7 +634,8 @@ __device__ __forceinline__ int swz(int row) {
 
 // IG >= 0 asks the compiler's instruction-group scheduler for strategy IG
 // (__builtin_amdgcn_iglp_opt) in the K loop; 1 interleaves the fragment reads
-// with the MFMAs of a single wave and was measured faster for 256x256 tiles.
+// with the MFMAs of a single wave and was measured faster for the 256x256 and
+// 128x128 tiles.
 template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 64, int WL = kWeightsRowMajor,
           int IG = -1>
 __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
@@ -978,7 +979,7 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
         if (mfma_ok) {
             switch (bm) {
                 case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(p, s);
-                case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL>(p, s);
+                case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL, 1>(p, s);
                 case 256: return launch_mfma<256, 256, 4, 4, 2, AM, EPI, 64, WL, 1>(p, s);
                 default: break;
             }
