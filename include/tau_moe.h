@@ -160,7 +160,9 @@ int tau_launch_moe_prefill_combine_ex(const void* contributions, void* output, c
 
 /* Whole routed path for any (E, K): routing, dispatch, gate_up+SiLU·mul,
  * down+weight, combine.  logits NULL: `routes` already holds the [T, 2K]
- * routes (tau_launch_moe_router_route_ex) and routing is skipped.  tile_rows from tau_moe_select_tile_rows (or any of
+ * routes (tau_launch_moe_router_route_ex, or E+1 experts and K+1 picks from
+ * tau_launch_moe_routing_shared_ex) and routing is skipped.  tile_rows from
+ * tau_moe_select_tile_rows (or any of
  * 16/32/64/128/256); weight_layout TAU_MOE_WEIGHTS_* for both weight tensors;
  * residual (may be NULL) is added in the combine as above (pass it here only
  * when no shared expert follows); receipts (optional) receive 10 words,
@@ -230,9 +232,10 @@ int tau_launch_centered_rms_norm(const void* input, const void* weight, void* ou
  * followed by the routing kernel (sparse_moe/routing.rs:91-93,125-231;
  * moe_routing.cu:15-52 generalised to any E <= 512, K <= 32): logits f32
  * [T, E] = input BF16 [T, H] . weight BF16 [E, H]^T (+ bias f32 [E], may be
- * NULL), exactly as tau_launch_moe_router_ex, then softmax / top-K /
- * renormalised weights into routes [T, 2K] as tau_launch_moe_routing_ex does
- * from those logits.  Two launches (projection with the bias fused; routing). */
+ * NULL), exactly as tau_launch_moe_router_ex, into `logits` (required), then
+ * softmax / top-K / renormalised weights into routes [T, 2K] as
+ * tau_launch_moe_routing_ex does from those logits.  Two launches (projection
+ * with the bias fused; routing). */
 int tau_launch_moe_router_route_ex(const void* input, const void* weight, const float* bias, float* logits,
                                    float* routes, int tokens, int hidden, int experts, int top_k, void* stream);
 
