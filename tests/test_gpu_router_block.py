@@ -189,3 +189,24 @@ def test_router_routing_rejects_bad_arguments(tau):
         tau.ffi.router_route_ex(w, w, None, logits, routes, 9)
     with pytest.raises(tau.ffi.LaunchError):  # no logits buffer
         tau.ffi.router_route_ex(w, w, None, None, routes, 2)
+
+
+@pytest.mark.parametrize("which", ["c2", "c3_t512", "c4_t300"])
+def test_block_is_deterministic_run_to_run(tau, which):
+    """No atomics in any reduction, a stable plan and a fixed-order K-split
+    router: repeated runs from hidden states are bit-identical (decode path,
+    general path with 128-row tiles, folded shared expert)."""
+    C = tau.inputs.CONFIGS
+    shape = {"c2": C["c2_30b_a3b_decode"], "c3_t512": tau.inputs.scaled(C["c3_30b_a3b_prefill"], 512),
+             "c4_t300": tau.inputs.scaled(C["c4_next_sparse"], 300)}[which]
+    say(f"[determinism] {shape.name}")
+    layer = tau.inputs.make_layer(shape)
+    shared = tau.SharedExpertConfig(shape.shared_intermediate) if shape.shared_intermediate else None
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k, shared_expert=shared)
+    blk = tau.SparseMoeBlock(cfg, layer["gate_up"], layer["down"], layer.get("shared_gate_up"),
+                             layer.get("shared_down"), layer.get("shared_gate"),
+                             router_weight=layer["router"].to(torch.bfloat16), router_bias=layer["bias"])
+    outs = [blk.forward(layer["x"]).clone() for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(torch.int16).cpu().numpy(), outs[0].view(torch.int16).cpu().numpy())
