@@ -613,6 +613,26 @@ __device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds) {
     const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u16)lds);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
 }
+// (hipcc warns that m0 is a reserved register in the clobber list.  These
+// kernels have no m0 access of the compiler's own: in the generated code of
+// grouped_gemm.hip every m0 write and read is inside these asm statements.)
+
+// The same copy addressed as a wave-uniform 64-bit base (SGPR pair) plus a
+// 32-bit per-lane byte offset: one VGPR per copy stream instead of two, and
+// the K advance moves only the scalar base.  Used by the 128x128 wave tiles,
+// whose 256 accumulators leave no room for 64-bit per-lane addresses.
+__device__ __forceinline__ void lds_dma16_off(const uint16_t* base, uint32_t off_bytes, uint16_t* lds) {
+    typedef __attribute__((address_space(3))) uint16_t* lds_u16;
+    const uint32_t lbase = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u16)lds);
+    const uint64_t g = (uint64_t)(uintptr_t)base;
+    // readfirstlane returns int: go through uint32_t so the low word is not
+    // sign-extended into the high one.
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
+    const uint64_t gs = ((uint64_t)hi << 32) | (uint64_t)lo;
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off_bytes), "s"(gs), "s"(lbase)
+                 : "memory", "m0");
+}
 
 // Workgroup barrier without the memory fence of __syncthreads (which waits
 // for every outstanding global load, in-flight LDS copies included).  Callers
@@ -643,6 +663,10 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int MI = TM / 32, NI = TN / 32;
     static_assert(MI >= 1 && NI >= 1, "wave tile too small");
+    // 128x128 wave tiles (256 accumulators, kept in AGPRs): operands are
+    // copied with 32-bit offsets from scalar bases and padding waves do not
+    // leave the K loop early, so the accumulators stay put across it.
+    constexpr bool kBigWave = TM * TN >= 128 * 128;
     static_assert(EPI != kEpiSilu || NI % 2 == 0, "SiLU pairs gate/up blocks");
     static_assert(EPI != kEpiStoreF32, "f32 outputs use lds_gemm");
     constexpr int CPR = BK / 8;                          // 16-byte chunks per staged row
@@ -658,7 +682,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     __shared__ long row_src[BM];   // gather: source row of A; down: destination slot (or -1)
     __shared__ float row_w[BM];    // down: route weight
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // Wave-uniform for the big wave tiles, which keeps the LDS stage addresses scalar.
+    const int wave = kBigWave ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     if (p.receipt && blockIdx.x == 0 && tid == 0) {
         p.receipt[0] = BM; p.receipt[1] = BN; p.receipt[2] = BK; p.receipt[3] = WM * WN; p.receipt[4] = STAGES;
@@ -734,6 +760,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     // q*RPI + l/CPR into chunk slot l%CPR, i.e. global chunk slot ^ swz(row).
     const int lrow8 = lane / CPR;
     const uint16_t* a_src[ACH];
+    uint32_t a_off[ACH];  // the same as byte offsets from p.a (big wave tiles)
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
         const int r = (i * (NT / 64) + wave) * RPI + lrow8;
@@ -746,6 +773,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             src_row = row0 + r < p.rows ? row0 + r : 0;
         }
         a_src[i] = p.a + src_row * (long)p.lda + kchunk;
+        a_off[i] = (uint32_t)((src_row * (long)p.lda + kchunk) * 2);
     }
     const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
     // Weight row of the B tile's row r (gate rows first, then up rows, for SiLU).
@@ -762,28 +790,38 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     // weights: instruction q copies one whole 1 KB fragment (16 rows x 32 of
     // K), so the B stage holds BN/16 bands x BK/32 fragments in global order.
     const uint16_t* b_src[BCH];
+    uint32_t b_off[BCH];  // the same as byte offsets from wexp (big wave tiles)
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
         const int q = i * (NT / 64) + wave;
+        long e_off;
         if constexpr (WL == kWeightsFrag16) {
             const int band = q / (BK / 32), c = q % (BK / 32);
-            b_src[i] = wexp + (weight_row(band * 16) >> 4) * 16L * p.k + c * 512 + lane * 8;
+            e_off = (weight_row(band * 16) >> 4) * 16L * p.k + c * 512 + lane * 8;
         } else {
             const int r = q * RPI + lrow8;
             const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
-            b_src[i] = wexp + weight_row(r) * (long)p.k + kchunk;
+            e_off = weight_row(r) * (long)p.k + kchunk;
         }
+        b_src[i] = wexp + e_off;
+        b_off[i] = (uint32_t)(e_off * 2);
     }
     auto issue = [&](int kt, int stage) {
         uint16_t* As = smem + stage * STAGE_ELEMS;
         uint16_t* Bs = As + BM * BK;
         const int kb = kt * BK;
 #pragma unroll
-        for (int i = 0; i < ACH; ++i)
-            if (a_live[i]) lds_dma16(a_src[i] + kb, As + (i * (NT / 64) + wave) * 512);
+        for (int i = 0; i < ACH; ++i) {
+            if (!a_live[i]) continue;
+            if constexpr (kBigWave) lds_dma16_off(p.a + kb, a_off[i], As + (i * (NT / 64) + wave) * 512);
+            else lds_dma16(a_src[i] + kb, As + (i * (NT / 64) + wave) * 512);
+        }
 #pragma unroll
-        for (int i = 0; i < BCH; ++i)
-            lds_dma16(b_src[i] + (WL == kWeightsFrag16 ? kb * 16 : kb), Bs + (i * (NT / 64) + wave) * 512);
+        for (int i = 0; i < BCH; ++i) {
+            const int kw = WL == kWeightsFrag16 ? kb * 16 : kb;
+            if constexpr (kBigWave) lds_dma16_off(wexp + kw, b_off[i], Bs + (i * (NT / 64) + wave) * 512);
+            else lds_dma16(b_src[i] + kw, Bs + (i * (NT / 64) + wave) * 512);
+        }
     };
 
     f32x16 acc[MI][NI];
@@ -838,7 +876,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
         const uint16_t* Bs = As + BM * BK;
-        if (!wave_rows_live) continue;
+        if constexpr (!kBigWave) {
+            if (!wave_rows_live) continue;
+        }
         if constexpr (IG >= 0) __builtin_amdgcn_iglp_opt(IG);
         bf16x8 af[2][MI], bfr[2][NI];
         frags(As, Bs, 0, af[0], bfr[0]);
@@ -878,6 +918,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
                 }
             }
         }
+        // Big wave tiles: keep each row block's accumulator reads next to
+        // their use (hoisting all 256 would exhaust the VGPRs).
+        if constexpr (kBigWave) __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
@@ -914,6 +957,12 @@ template <int BM, int BN, int WM, int WN, int STAGES, int AM, int EPI, int BK = 
           int IG = -1>
 int launch_mfma(const GemmArgs& p, hipStream_t s) {
     constexpr int NOUT = EPI == kEpiSilu ? BN / 2 : BN;
+    if constexpr ((BM / WM) * (BN / WN) >= 128 * 128) {
+        // 32-bit operand offsets: the A rows and one expert's weights must
+        // span less than 4 GiB.
+        const long a_rows = AM == kAGather ? (long)p.assignments / p.topk : (long)p.rows;
+        if (a_rows * (long)p.lda * 2 >= (1L << 32) || p.w_expert_stride * 2 >= (1L << 32)) return kInvalid;
+    }
     const long m_blocks = (p.rows + BM - 1) / BM;
     const long n_tiles = (p.n + NOUT - 1) / NOUT;
     const long grid = (m_blocks * n_tiles + kXcds - 1) / kXcds * kXcds;
@@ -972,6 +1021,13 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
 // waves, wave tile 64x64), measured best on MI355X for the prefill shapes; shapes the MFMA
 // kernel cannot take (K not a multiple of 64, unaligned rows, FP32 output)
 // use the register-staged LDS kernel, which reads row-major weights only.
+// 256x256 tiles: 4x4 waves of 64x64 (the measured default) or, built with
+// -DTAU_M256_BIG_WAVES, 2x2 waves of 128x128 with AGPR accumulators.
+#ifdef TAU_M256_BIG_WAVES
+constexpr int kM256WavesM = 2, kM256WavesN = 2;
+#else
+constexpr int kM256WavesM = 4, kM256WavesN = 4;
+#endif
 template <int AM, int EPI, int WL>
 int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
     const bool mfma_ok = aligned && p.k % 64 == 0 && EPI != kEpiStoreF32;
@@ -980,7 +1036,7 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
             switch (bm) {
                 case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(p, s);
                 case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL, 1>(p, s);
-                case 256: return launch_mfma<256, 256, 4, 4, 2, AM, EPI, 64, WL, 1>(p, s);
+                case 256: return launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(p, s);
                 default: break;
             }
         }
