@@ -17,8 +17,9 @@
  *   - data errors (non-finite logits, malformed routes) never fail a launch:
  *     they set the plan's status word and every output element becomes NaN;
  *   - BF16 tensors are raw uint16 bit patterns; routes are f32 [T, 2K]
- *     (K expert ids stored as floats, then K normalised weights); meta is
- *     int32 [2E+2] = counts[E], cursors[E], status, padded row total.
+ *     (K expert ids stored as floats, then K weights, renormalised unless
+ *     TAU_MOE_ROUTE_RAW_WEIGHTS is set); meta is int32 [2E+2] = counts[E],
+ *     cursors[E], status, padded row total.
  *
  * Reference interfaces replaced (paths relative to the tau.rs root):
  *   crates/cuda-kernels/src/cuda_ffi.rs (declarations) and the CUDA
@@ -142,7 +143,16 @@ int tau_moe_select_tile_rows(int tokens, int experts, int top_k, int hidden, int
 int tau_moe_workspace_bytes(int tokens, int hidden, int intermediate, int experts, int top_k, int tile_rows,
                             size_t out_bytes[7]);
 
-/* Router softmax/top-k; logits_dtype 0 = f32, 1 = BF16; routes f32 [T, 2K]. */
+/* Flag OR-ed into any logits_dtype argument: route weights are the selected
+ * softmax probabilities as they are, not renormalised by their sum
+ * (normalize_selected_weights = false; sparse_moe/config.rs:45,
+ * sparse_moe/routing.rs:198-202).  Without it weights are renormalised. */
+#define TAU_MOE_ROUTE_RAW_WEIGHTS 0x100
+
+/* Router softmax/top-k; logits_dtype 0 = f32, 1 = BF16 (| TAU_MOE_ROUTE_RAW_WEIGHTS);
+ * routes f32 [T, 2K].  Experts are ranked on their f32 softmax probabilities
+ * (exp with glibc expf's results, the sum in expert order), larger first and
+ * the lower id on equal probabilities, as routing.rs:125-257. */
 int tau_launch_moe_routing_ex(const void* logits, int logits_dtype, float* routes, int tokens, int experts,
                               int top_k, void* stream);
 

@@ -400,6 +400,12 @@ void oracle_dense_mlp(const float* x, int T, int H, int I,
     }
 }
 
+/* The shared expert's gate, sigmoid(v) = 1 / (1 + exp(-v)) in f32
+ * (candle's sigmoid op at shared_expert.rs:155), elementwise. */
+void oracle_sigmoid(const float* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = 1.0f / (1.0f + expf(-in[i]));
+}
+
 /* Shared-expert combine, f32 CPU path (shared_expert.rs:68,142-159):
  * out = routed + shared * sigmoid(x . w_s), with the product and the sum
  * rounded separately.  gate_weight NULL means an ungated shared expert. */

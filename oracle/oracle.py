@@ -73,6 +73,8 @@ def lib():
         _lib.oracle_linear_f32.restype = None
         _lib.oracle_bf16_round_array.argtypes = [f, f, i64]
         _lib.oracle_bf16_round_array.restype = None
+        _lib.oracle_sigmoid.argtypes = [f, f, i64]
+        _lib.oracle_sigmoid.restype = None
         _lib.oracle_set_threads.argtypes = [i]
         _lib.oracle_centered_rms_norm.argtypes = [f, f, f, f, f, i, i, ctypes.c_float, i]
         _lib.oracle_centered_rms_norm.restype = None
@@ -197,6 +199,14 @@ def dense_mlp(x, gate_up, down, act: int = ACT_SILU, bf16: bool = False) -> np.n
     i = gate_up.shape[0] // 2
     out = np.zeros((t, h), dtype=np.float32)
     lib().oracle_dense_mlp(_p(x), t, h, i, _p(gate_up), _p(down), int(act), int(bool(bf16)), _p(out))
+    return out
+
+
+def sigmoid(v) -> np.ndarray:
+    """f32 1 / (1 + exp(-v)) elementwise, the shared expert's gate."""
+    v = _f32(v)
+    out = np.empty_like(v)
+    lib().oracle_sigmoid(_p(v), _p(out), v.size)
     return out
 
 

@@ -6,6 +6,7 @@
 #include <algorithm>
 
 #include "kernels.hpp"
+#include "libm_expf.hpp"
 
 namespace tau_amd {
 namespace {
@@ -39,6 +40,19 @@ __device__ __forceinline__ float row_sum(float v) {
     v += dppf<kRowHalfMirror>(v);
     v += dppf<kRowMirror>(v);
     return v;
+}
+
+// Sum of p[j] over the row's values in expert order e = 16 j + lane, one
+// element at a time (((p_0 + p_1) + p_2) + ...): the sequential f32 sum of the
+// reference's softmax denominator.  Each step is one v_add_f32 with a DPP
+// row_newbcast operand (lane L of the row broadcast to all 16 lanes).
+template <int L, int EP>
+__device__ __forceinline__ float row_sum_in_order(const float (&p)[EP], float acc) {
+    if constexpr (L == 16 * EP) {
+        return acc;
+    } else {
+        return row_sum_in_order<L + 1, EP>(p, acc + dppf<0x150 + (L & 15)>(p[L >> 4]));
+    }
 }
 
 __device__ __forceinline__ uint32_t row_or(uint32_t v) {
@@ -87,14 +101,18 @@ __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p, size_t 
 // and, when `eids` is non-null, the K selected experts (or -1 for every rank
 // of a rejected row) at eids[0..K).  Returns true when the row was rejected.
 // Rows with `active == false` take part in the DPP steps but write nothing.
+// `normalize`: weights p / (rank-ordered sum of the K selected p), else the
+// selected probabilities as they are (normalize_selected_weights of
+// sparse_moe/config.rs:45, applied at routing.rs:198-202).
 // Layout overrides (0 = default): `ldl` logits per row (E), `routes_stride`
 // floats per routes row (2K) and `weights_ofs` offset of the weights in it (K).
 template <int EP, typename T>
 __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, float* routes, int E, int K,
-                                          int* eids, int ldl = 0, int routes_stride = 0, int weights_ofs = 0) {
+                                          int* eids, bool normalize, int ldl = 0, int routes_stride = 0,
+                                          int weights_ofs = 0) {
     const int l16 = threadIdx.x & 15;
     const T* row = logits + (size_t)(active ? t : 0) * (ldl ? ldl : E);
-    float d[EP], p[EP];  // p: exp(x - max) numerators
+    float d[EP], p[EP];  // logits; softmax probabilities
     uint32_t nonfinite = 0;
     float maximum = -INFINITY;
     // Unconditional loads (clamped index) so all EP loads are in flight at
@@ -113,15 +131,19 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
     }
     nonfinite = row_or(nonfinite);
     maximum = row_max(maximum);
-    float local = 0.f;
+    // Softmax as the reference's f32 CPU path computes it: numerators
+    // exp(x - max) with glibc's expf bits, their sum in expert order, one
+    // division each.  Experts are then ranked on these probabilities, so
+    // distinct logits whose probabilities round equal tie to the lower id
+    // exactly as routing.rs:239-257 does.
 #pragma unroll
     for (int j = 0; j < EP; ++j) {
         const int e = j * 16 + l16;
-        d[j] = (d[j] - maximum) + 0.0f;  // -0 folded onto +0: equal values, equal keys
-        p[j] = e < E ? expf(d[j]) : 0.f;  // numerators; divided only once selected
-        local += p[j];
+        p[j] = e < E ? expf_glibc(d[j] - maximum) : 0.f;
     }
-    const float denominator = row_sum(local);
+    const float denominator = row_sum_in_order<0, EP>(p, 0.f);
+#pragma unroll
+    for (int j = 0; j < EP; ++j) p[j] = p[j] / denominator;
 
     float selected_sum = 0.f;
     int my_id[2] = {0, 0};
@@ -129,10 +151,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
     // Rank r's pick is published to lane r % 16 of the row (slot r / 16).
     auto publish = [&](int r, uint64_t best) {
         const int id = (int)(0xffffffffu - (uint32_t)best);
-        // Softmax probability exp(x - max) / sum: exp of the very value the key
-        // was made from (orderable() is a bijection), so it equals the
-        // numerator summed above bit for bit.
-        const float prob = expf(from_orderable((uint32_t)(best >> 32))) / denominator;
+        const float prob = from_orderable((uint32_t)(best >> 32));  // the key is the probability
         selected_sum += prob;  // rank order, as routing.rs:187-191
         if (l16 == (r & 15)) {
             if (r < 16) { my_id[0] = id; my_p[0] = prob; }
@@ -140,7 +159,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
         }
     };
     // pick(): the next expert of the row by (probability desc, id asc), as a
-    // 64-bit key (orderable(x - max), ~id) identical on all 16 lanes.
+    // 64-bit key (orderable(probability), ~id) identical on all 16 lanes.
     // Up to 16 keys per lane: each lane sorts its keys once (bitonic network,
     // descending) and a pick is the row max of the lane heads; its owner
     // advances.  32 keys per lane: a strict '>' scan over the untaken 32-bit
@@ -153,7 +172,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
 #pragma unroll
         for (int j = 0; j < EP; ++j) {
             const int e = j * 16 + l16;
-            key[j] = e < E ? ((uint64_t)orderable(d[j]) << 32) | (0xffffffffu - (uint32_t)e) : 0;
+            key[j] = e < E ? ((uint64_t)orderable(p[j]) << 32) | (0xffffffffu - (uint32_t)e) : 0;
         }
 #pragma unroll
         for (int size = 2; size <= EP; size <<= 1)
@@ -171,7 +190,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
                 }
     } else {
 #pragma unroll
-        for (int j = 0; j < EP; ++j) ord[j] = j * 16 + l16 < E ? orderable(d[j]) : 0u;  // valid values are > 0
+        for (int j = 0; j < EP; ++j) ord[j] = j * 16 + l16 < E ? orderable(p[j]) : 0u;  // valid values are > 0
     }
     auto pick = [&]() -> uint64_t {
         if constexpr (EP <= 16) {
@@ -211,7 +230,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
             picked = l16 == r ? best : picked;
         }
         const bool ranked = l16 < K;
-        const float prob = ranked ? expf(from_orderable((uint32_t)(picked >> 32))) / denominator : 0.f;
+        const float prob = ranked ? from_orderable((uint32_t)(picked >> 32)) : 0.f;
         // Left fold p0 + p1 + ... + p(K-1), as the sequential loop of
         // routing.rs:187-191: lane r adds its p to lane r-1's partial.
         float partial = prob;
@@ -234,7 +253,7 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
             const int rank = s * 16 + l16;
             if (rank < K) {
                 out[rank] = nonfinite ? __builtin_nanf("") : (float)my_id[s];
-                out[wofs + rank] = nonfinite ? __builtin_nanf("") : my_p[s] / selected_sum;
+                out[wofs + rank] = nonfinite ? __builtin_nanf("") : normalize ? my_p[s] / selected_sum : my_p[s];
                 if (eids) eids[rank] = nonfinite ? -1 : my_id[s];
             }
         }
@@ -245,9 +264,10 @@ __device__ __forceinline__ bool route_row(const T* logits, int t, bool active, f
 // One wavefront (four tokens) per workgroup, so small batches still spread
 // over every CU.
 template <int EP, typename T>
-__global__ __launch_bounds__(64) void route_kernel(const T* logits, float* routes, int T_, int E, int K) {
+__global__ __launch_bounds__(64) void route_kernel(const T* logits, float* routes, int T_, int E, int K,
+                                                   int normalize) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
-    route_row<EP, T>(logits, t, t < T_, routes, E, K, nullptr);
+    route_row<EP, T>(logits, t, t < T_, routes, E, K, nullptr, normalize != 0);
 }
 
 // Routing with an always-on shared expert folded in as expert E: logits rows
@@ -256,16 +276,18 @@ __global__ __launch_bounds__(64) void route_kernel(const T* logits, float* route
 // sigmoid(gate)), in rows of 2(K+1) floats.  A rejected routed row (or a
 // non-finite gate, through its weight) invalidates the plan as before.
 template <int EP, typename T>
-__global__ __launch_bounds__(64) void route_shared_kernel(const T* logits, float* routes, int T_, int E, int K) {
+__global__ __launch_bounds__(64) void route_shared_kernel(const T* logits, float* routes, int T_, int E, int K,
+                                                          int normalize) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
     const bool active = t < T_;
     const int K1 = K + 1;
-    const bool bad = route_row<EP, T>(logits, t, active, routes, E, K, nullptr, E + 1, 2 * K1, K1);
+    const bool bad = route_row<EP, T>(logits, t, active, routes, E, K, nullptr, normalize != 0, E + 1, 2 * K1, K1);
     if (active && (threadIdx.x & 15) == 0) {
         const float gate = load_logit<T>(logits, (size_t)t * (E + 1) + E);
         float* out = routes + (size_t)t * 2 * K1;
         out[K] = bad ? __builtin_nanf("") : (float)E;
-        out[K1 + K] = bad ? __builtin_nanf("") : sigmoid(gate);
+        // sigmoid 1 / (1 + exp(-g)) with glibc's exp bits, as the f32 CPU path
+        out[K1 + K] = bad ? __builtin_nanf("") : 1.0f / (1.0f + expf_glibc(-gate));
     }
 }
 
@@ -311,6 +333,7 @@ __device__ __forceinline__ uint64_t match_expert(int e, bool active, int bits) {
 struct DispatchArgs {
     const void* logits;  // routing input (null: routes given)
     int logits_bf16;
+    int normalize;  // renormalise the selected weights (routing from logits only)
     float* routes;
     int* meta;
     int* offsets;
@@ -518,9 +541,11 @@ __device__ void route_span(const DispatchArgs& p, const DispatchLds& l, int t0, 
         const bool active = t < t1;
         int* eids = l.eids + (size_t)(t - t0) * p.K;
         if (p.logits_bf16)
-            bad |= route_row<EP, uint16_t>((const uint16_t*)p.logits, t, active, p.routes, p.E, p.K, eids) && active;
+            bad |= route_row<EP, uint16_t>((const uint16_t*)p.logits, t, active, p.routes, p.E, p.K, eids,
+                                                 p.normalize != 0) && active;
         else
-            bad |= route_row<EP, float>((const float*)p.logits, t, active, p.routes, p.E, p.K, eids) && active;
+            bad |= route_row<EP, float>((const float*)p.logits, t, active, p.routes, p.E, p.K, eids,
+                                                 p.normalize != 0) && active;
     }
     if (bad) l.flag[0] = 1;
 }

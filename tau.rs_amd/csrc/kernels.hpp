@@ -41,6 +41,8 @@ bool gemm_rows_supported(int bm);
 int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M);
 int launch_routing_shared(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                           hipStream_t s);
+// logits_dtype 0 (f32) or 1 (BF16), optionally OR TAU_MOE_ROUTE_RAW_WEIGHTS.
+bool logits_dtype_ok(int logits_dtype);
 int launch_routing(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                    hipStream_t s);
 int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* meta, int* offsets, int* slots,

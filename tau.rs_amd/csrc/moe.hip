@@ -272,7 +272,7 @@ int tau_launch_moe_prefill_ex(const void* input, const void* logits, int logits_
     if (!input || !gate_up || !down || !routes || !meta || !offsets || !slots || !tiles || !activated ||
         !contributions || !output || !shape_ok(tokens, hidden, intermediate, experts, top_k) ||
         !layout_ok(weight_layout, hidden, intermediate) ||
-        (logits && ((logits_dtype != 0 && logits_dtype != 1) || experts > 512)) ||
+        (logits && (!logits_dtype_ok(logits_dtype) || experts > 512)) ||
         !gemm_rows_supported(tile_rows) || capacity < capacity_for(tokens, experts, top_k, tile_rows) ||
         capacity % tile_rows)
         return kInvalid;

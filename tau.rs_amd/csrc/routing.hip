@@ -11,12 +11,14 @@
 //
 // CDNA4 design.
 //  * Routing: one 16-lane DPP row per token, four tokens per wavefront.  Each
-//    lane owns E/16 logits; max, sum and the K arg-max steps are row-local DPP
+//    lane owns E/16 logits; the max and the K arg-max steps are row-local DPP
 //    butterflies (quad_perm, row_half_mirror, row_mirror), so a top-K costs no
 //    LDS or cross-lane memory traffic and the four tokens of a wave proceed
-//    together.  Ordering keys are (x - max, ~id) in 64 bits: exp is monotone,
-//    so they order experts exactly as the probabilities do, ties included,
-//    whatever the rounding of exp.
+//    together.  The softmax is the reference's f32 one bit for bit: exp with
+//    glibc expf's results (libm_expf.hpp), the denominator summed in expert
+//    order (one DPP-broadcast add per expert), one division per expert.
+//    Ordering keys are (probability, ~id) in 64 bits, so distinct logits whose
+//    probabilities round equal tie to the lower id, as in the reference.
 //  * Dispatch: a counting sort.  Every assignment's expert is staged in LDS,
 //    16 waves each count a contiguous segment (ballot-derived peer masks, no
 //    global atomics), counts are prefixed per expert over waves and over
@@ -32,15 +34,15 @@ namespace tau_amd {
 namespace {
 
 template <typename T>
-int launch_route(const T* logits, float* routes, int tokens, int E, int K, hipStream_t s) {
+int launch_route(const T* logits, float* routes, int tokens, int E, int K, int normalize, hipStream_t s) {
     const int blocks = (tokens + 3) / 4;
     const int ep = (E + 15) / 16;
-    if (ep <= 1) route_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 2) route_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 4) route_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 8) route_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 16) route_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else route_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    if (ep <= 1) route_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 2) route_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 4) route_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 8) route_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 16) route_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else route_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
     return (int)hipGetLastError();
 }
 
@@ -85,27 +87,34 @@ int64_t capacity_for(int64_t tokens, int64_t E, int64_t K, int64_t M) {
     return bound / M * M;
 }
 
+// logits_dtype: 0 = f32, 1 = BF16, optionally OR TAU_MOE_ROUTE_RAW_WEIGHTS.
+bool logits_dtype_ok(int logits_dtype) {
+    const int dtype = logits_dtype & ~TAU_MOE_ROUTE_RAW_WEIGHTS;
+    return dtype == 0 || dtype == 1;
+}
+
 int launch_routing(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                    hipStream_t s) {
     if (!logits || !routes || tokens <= 0 || E <= 0 || E > kMaxExperts || K <= 0 || K > E || K > kMaxTopK ||
-        (logits_dtype != 0 && logits_dtype != 1))
+        !logits_dtype_ok(logits_dtype))
         return kInvalid;
-    if (logits_dtype == 1) return launch_route<uint16_t>((const uint16_t*)logits, routes, tokens, E, K, s);
-    return launch_route<float>((const float*)logits, routes, tokens, E, K, s);
+    const int normalize = !(logits_dtype & TAU_MOE_ROUTE_RAW_WEIGHTS);
+    if (logits_dtype & 1) return launch_route<uint16_t>((const uint16_t*)logits, routes, tokens, E, K, normalize, s);
+    return launch_route<float>((const float*)logits, routes, tokens, E, K, normalize, s);
 }
 
 namespace {
 
 template <typename T>
-int launch_route_shared(const T* logits, float* routes, int tokens, int E, int K, hipStream_t s) {
+int launch_route_shared(const T* logits, float* routes, int tokens, int E, int K, int normalize, hipStream_t s) {
     const int blocks = (tokens + 3) / 4;
     const int ep = (E + 15) / 16;
-    if (ep <= 1) route_shared_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 2) route_shared_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 4) route_shared_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 8) route_shared_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else if (ep <= 16) route_shared_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
-    else route_shared_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K);
+    if (ep <= 1) route_shared_kernel<1, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 2) route_shared_kernel<2, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 4) route_shared_kernel<4, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 8) route_shared_kernel<8, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else if (ep <= 16) route_shared_kernel<16, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
+    else route_shared_kernel<32, T><<<blocks, 64, 0, s>>>(logits, routes, tokens, E, K, normalize);
     return (int)hipGetLastError();
 }
 
@@ -116,10 +125,12 @@ int launch_route_shared(const T* logits, float* routes, int tokens, int E, int K
 int launch_routing_shared(const void* logits, int logits_dtype, float* routes, int tokens, int E, int K,
                           hipStream_t s) {
     if (!logits || !routes || tokens <= 0 || E <= 0 || E > kMaxExperts || K <= 0 || K > E || K + 1 > kMaxTopK ||
-        (logits_dtype != 0 && logits_dtype != 1))
+        !logits_dtype_ok(logits_dtype))
         return kInvalid;
-    if (logits_dtype == 1) return launch_route_shared<uint16_t>((const uint16_t*)logits, routes, tokens, E, K, s);
-    return launch_route_shared<float>((const float*)logits, routes, tokens, E, K, s);
+    const int normalize = !(logits_dtype & TAU_MOE_ROUTE_RAW_WEIGHTS);
+    if (logits_dtype & 1)
+        return launch_route_shared<uint16_t>((const uint16_t*)logits, routes, tokens, E, K, normalize, s);
+    return launch_route_shared<float>((const float*)logits, routes, tokens, E, K, normalize, s);
 }
 
 // Dispatch; with logits, routing runs inside the plan kernels.  `scratch`
@@ -134,10 +145,11 @@ int launch_dispatch(const void* logits, int logits_dtype, float* routes, int* me
         return kInvalid;
     if ((int64_t)tokens * K > (int64_t)1 << 30) return kInvalid;
     if ((int64_t)capacity < capacity_for(tokens, E, K, M)) return kInvalid;
-    if (logits && logits_dtype != 0 && logits_dtype != 1) return kInvalid;
+    if (logits && !logits_dtype_ok(logits_dtype)) return kInvalid;
     DispatchArgs a{};
     a.logits = logits;
-    a.logits_bf16 = logits_dtype == 1;
+    a.logits_bf16 = logits_dtype & 1;
+    a.normalize = !(logits_dtype & TAU_MOE_ROUTE_RAW_WEIGHTS);
     a.routes = routes;
     a.meta = meta;
     a.offsets = offsets;

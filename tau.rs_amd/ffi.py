@@ -143,11 +143,15 @@ def check(code: int, kernel: str) -> None:
         raise LaunchError(code, kernel)
 
 
-def _dtype_code(t: torch.Tensor) -> int:
+ROUTE_RAW_WEIGHTS = 0x100  # TAU_MOE_ROUTE_RAW_WEIGHTS: keep the selected probabilities unnormalised
+
+
+def _dtype_code(t: torch.Tensor, raw_weights: bool = False) -> int:
+    flag = ROUTE_RAW_WEIGHTS if raw_weights else 0
     if t.dtype == torch.float32:
-        return 0
+        return 0 | flag
     if t.dtype == torch.bfloat16:
-        return 1
+        return 1 | flag
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
@@ -166,26 +170,27 @@ def workspace_bytes(tokens, hidden, intermediate, experts, top_k, tile_rows):
     return list(out)
 
 
-def routing_ex(logits, routes, experts, top_k, stream=None):
+def routing_ex(logits, routes, experts, top_k, stream=None, raw_weights=False):
     t = logits.shape[0]
-    check(lib().tau_launch_moe_routing_ex(ptr(logits), _dtype_code(logits), ptr(routes), t, experts, top_k,
+    check(lib().tau_launch_moe_routing_ex(ptr(logits), _dtype_code(logits, raw_weights), ptr(routes), t, experts,
+                                          top_k,
                                           stream_ptr(stream)), "MoE routing")
 
 
 def dispatch_ex(logits, routes, meta, offsets, slots, tiles, tokens, experts, top_k, tile_rows, cap,
-                stream=None):
+                stream=None, raw_weights=False):
     code = lib().tau_launch_moe_prefill_dispatch_ex(
-        ptr(logits), _dtype_code(logits) if logits is not None else 0, ptr(routes), ptr(meta), ptr(offsets),
+        ptr(logits), _dtype_code(logits, raw_weights) if logits is not None else 0, ptr(routes), ptr(meta), ptr(offsets),
         ptr(slots), ptr(tiles), tokens, experts, top_k, tile_rows, cap, stream_ptr(stream))
     check(code, "MoE dispatch")
 
 
 def prefill_ex(x, logits, gate_up, down, ws, output, experts, top_k, tile_rows, receipts=None, stream=None,
-               weight_layout=WEIGHTS_ROW_MAJOR, residual=None):
+               weight_layout=WEIGHTS_ROW_MAJOR, residual=None, raw_weights=False):
     t, h = x.shape
     i = down.shape[2]
     code = lib().tau_launch_moe_prefill_ex(
-        ptr(x), ptr(logits), _dtype_code(logits) if logits is not None else 0, ptr(gate_up), ptr(down),
+        ptr(x), ptr(logits), _dtype_code(logits, raw_weights) if logits is not None else 0, ptr(gate_up), ptr(down),
         ptr(ws["routes"]), ptr(ws["meta"]),
         ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]), ptr(ws["activated"]),
         ptr(ws["contributions"]), ptr(output), t, h, i, experts, top_k, tile_rows, ws["capacity"],
@@ -230,24 +235,34 @@ def pack_weights(w: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 def router_route_ex(x: torch.Tensor, weight: torch.Tensor, bias, logits: torch.Tensor, routes: torch.Tensor,
-                    top_k: int, stream=None):
-    """logits f32 [T, E] and routes [T, 2K] from x BF16 [T, H] in one call."""
+                    top_k: int, stream=None, raw_weights=False):
+    """logits f32 [T, E] and routes [T, 2K] from x BF16 [T, H] in one call
+    (two calls, projection then routing, for unnormalised weights)."""
     t, h = x.shape
     e = weight.shape[0]
+    if raw_weights:
+        router_ex(x, weight, bias, logits, stream=stream)
+        routing_ex(logits, routes, e, top_k, stream=stream, raw_weights=True)
+        return
     check(lib().tau_launch_moe_router_route_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(routes), t, h, e,
                                                top_k, stream_ptr(stream)), "MoE router + routing")
 
 
-def routing_shared_ex(logits, routes, experts, top_k, stream=None):
+def routing_shared_ex(logits, routes, experts, top_k, stream=None, raw_weights=False):
     """routes [T, 2(K+1)] from logits [T, E+1]: routed top-K, then (E, sigmoid(gate))."""
     t = logits.shape[0]
-    check(lib().tau_launch_moe_routing_shared_ex(ptr(logits), _dtype_code(logits), ptr(routes), t, experts, top_k,
+    check(lib().tau_launch_moe_routing_shared_ex(ptr(logits), _dtype_code(logits, raw_weights), ptr(routes), t,
+                                                 experts, top_k,
                                                  stream_ptr(stream)), "MoE routing with shared expert")
 
 
-def router_route_shared_ex(x, weight, bias, logits, routes, experts, top_k, stream=None):
+def router_route_shared_ex(x, weight, bias, logits, routes, experts, top_k, stream=None, raw_weights=False):
     """logits f32 [T, E+1] and routes [T, 2(K+1)] from x BF16 [T, H]; weight [E+1, H]."""
     t, h = x.shape
+    if raw_weights:
+        router_ex(x, weight, bias, logits, stream=stream)
+        routing_shared_ex(logits, routes, experts, top_k, stream=stream, raw_weights=True)
+        return
     check(lib().tau_launch_moe_router_route_shared_ex(ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(routes), t, h,
                                                       experts, top_k, stream_ptr(stream)),
           "MoE router + routing with shared expert")

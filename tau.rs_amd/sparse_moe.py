@@ -51,8 +51,6 @@ class SparseMoeConfig:
             raise ValueError("sparse MoE experts_per_token cannot exceed num_experts")
         if self.shared_expert is not None and self.shared_expert.intermediate_size == 0:
             raise ValueError("sparse MoE shared-expert intermediate size must be non-zero")
-        if not self.normalize_selected_weights:
-            raise ValueError("the HIP path implements normalised top-k weights only")
         if self.num_experts > 512 or self.experts_per_token > 32:
             raise ValueError("the HIP path supports num_experts <= 512 and experts_per_token <= 32")
 
@@ -133,6 +131,7 @@ class MoePrefillRunner:
         if gate_up.dtype != torch.bfloat16 or down.dtype != torch.bfloat16 or not gate_up.is_cuda:
             raise ValueError("the HIP path takes contiguous BF16 device weights")
         self.config = config
+        self.raw_weights = not config.normalize_selected_weights
         packable = H % 64 == 0 and I % 64 == 0
         if weight_layout not in ("auto", "row_major", "frag16"):
             raise ValueError(f"unknown weight layout {weight_layout!r}")
@@ -223,7 +222,7 @@ class MoePrefillRunner:
             logits = logits.contiguous()
         ffi.prefill_ex(x, logits, self.gate_up, self.down, ws, out, c.num_experts,
                        c.experts_per_token, tile_rows, receipts=self._receipts, stream=stream,
-                       weight_layout=self.layout, residual=residual)
+                       weight_layout=self.layout, residual=residual, raw_weights=self.raw_weights)
         self._calls += 1
         return out
 
@@ -325,9 +324,11 @@ class SparseMoeBlock:
         w, b = self.router
         logits = self._logits_buffer(x.shape[0], x.device)
         E, K = self.config.num_experts, self.config.experts_per_token
+        raw = not self.config.normalize_selected_weights
         if self.folded:
-            return lambda routes: ffi.router_route_shared_ex(x, w, b, logits, routes, E, K, stream=stream)
-        return lambda routes: ffi.router_route_ex(x, w, b, logits, routes, K, stream=stream)
+            return lambda routes: ffi.router_route_shared_ex(x, w, b, logits, routes, E, K, stream=stream,
+                                                             raw_weights=raw)
+        return lambda routes: ffi.router_route_ex(x, w, b, logits, routes, K, stream=stream, raw_weights=raw)
 
     def _shared_routes(self, x: torch.Tensor, logits: torch.Tensor, stream=None):
         """routes(routes_buffer) from caller logits for the folded shared expert:
@@ -344,7 +345,8 @@ class SparseMoeBlock:
             ext = torch.cat([logits.float(), gate], 1) if logits.dtype != torch.float32 else torch.cat([logits, gate], 1)
         else:
             raise ValueError("router logits must be [tokens, num_experts] (or + 1 shared gate column)")
-        return lambda routes: ffi.routing_shared_ex(ext, routes, E, K, stream=stream)
+        raw = not self.config.normalize_selected_weights
+        return lambda routes: ffi.routing_shared_ex(ext, routes, E, K, stream=stream, raw_weights=raw)
 
     def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, stream=None,
                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:

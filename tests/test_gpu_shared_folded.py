@@ -38,7 +38,7 @@ def rel_l2(a, b):
 
 @pytest.mark.parametrize("t,e,k,dtype", [(64, 128, 8, torch.float32), (37, 512, 10, torch.float32),
                                          (100, 60, 20, torch.bfloat16), (5, 16, 4, torch.bfloat16)])
-def test_shared_routing_ranks(tau, t, e, k, dtype):
+def test_shared_routing_ranks(tau, oracle, t, e, k, dtype):
     say(f"[shared routing] T={t} E={e} K={k} {dtype}")
     g = torch.Generator(device="cuda").manual_seed(t + e)
     logits = (torch.randn(t, e + 1, generator=g, device="cuda") * 2).to(dtype)
@@ -58,6 +58,8 @@ def test_shared_routing_ranks(tau, t, e, k, dtype):
     gate = f32(logits[:, e]).astype(np.float64)
     sig = 1.0 / (1.0 + np.exp(-gate))
     assert np.all(np.abs(r[~bad, 2 * k + 1] - sig[~bad]) <= 2e-7 + 2e-6 * sig[~bad])
+    # bit for bit the f32 sigmoid of the reference's CPU path
+    np.testing.assert_array_equal(r[~bad, 2 * k + 1], oracle.sigmoid(f32(logits[:, e]))[~bad])
 
 
 def block_pair(tau, shape, router=False):

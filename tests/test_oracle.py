@@ -90,6 +90,53 @@ def test_router_weight_on_feature_zero_closed_form():
     assert list(ids[2]) == list(range(8))
 
 
+def test_unnormalised_weights_are_the_softmax_probabilities():
+    # normalize_selected_weights = false (sparse_moe/config.rs:45, routing.rs:198-202):
+    # the weights are the selected probabilities themselves; torch's f32 softmax
+    # (an independent implementation) agrees to f32 rounding, and the
+    # normalised weights are exactly those divided by their rank-ordered sum.
+    rng = np.random.default_rng(7)
+    lg = rng.standard_normal((64, 48)).astype(np.float32) * 3
+    ids, raw = O.route(lg, 6, normalize=False)
+    ids_n, w_n = O.route(lg, 6)
+    np.testing.assert_array_equal(ids, ids_n)
+    probs = torch.softmax(torch.from_numpy(lg).double(), -1).numpy()
+    sel = np.take_along_axis(probs, ids.astype(np.int64), 1)
+    assert np.all(np.abs(raw - sel) <= 1e-6 * sel + 1e-12)  # f32 rounding of exp, sum and quotient
+    for t in range(lg.shape[0]):
+        total = np.float32(0)
+        for r in range(6):
+            total = np.float32(total + raw[t, r])
+        np.testing.assert_array_equal(w_n[t], (raw[t] / total).astype(np.float32))
+    _, raw_all = O.route(lg, 48, normalize=False)
+    assert np.all(np.abs(raw_all.astype(np.float64).sum(1) - 1) < 1e-5)
+
+
+def test_experts_rank_on_probabilities_so_collapsed_logits_tie_to_lower_id():
+    # routing.rs:139-141,239-257 compare f32 probabilities, not logits: two
+    # distinct logits whose exp(x - max) rounds to the same float are a tie,
+    # which the lower id wins even when its logit is the smaller one.
+    # exp(-2^-25) = 1 - 2^-25 is halfway between 1 - 2^-24 and 1 and rounds to 1.
+    tiny = np.float32(2.0 ** -25)
+    lg = np.array([[-tiny, 0.0, -4.0, -5.0],      # id 0 has the smaller logit
+                   [0.0, -tiny, -4.0, -5.0],
+                   [-5.0, -4.0, 0.0, -np.float32(2.0 ** -23)]], np.float32)
+    ids, w, p = O.route(lg, 2, want_probabilities=True)
+    assert p[0, 0] == p[0, 1] and p[1, 0] == p[1, 1]
+    assert list(ids[0]) == [0, 1] and list(ids[1]) == [0, 1]
+    assert w[0, 0] == w[0, 1] == np.float32(0.5)
+    # a 2^-23 gap survives exp (1 - 2^-23 is a float): the larger logit leads
+    assert p[2, 2] > p[2, 3] and list(ids[2]) == [2, 3]
+
+
+def test_sigmoid_gate_matches_f64_and_closed_forms():
+    v = np.concatenate([np.linspace(-30, 30, 2001), [0.0, -200.0, 200.0, -np.inf, np.inf]]).astype(np.float32)
+    s = O.sigmoid(v)
+    ref = 1.0 / (1.0 + np.exp(-v.astype(np.float64)))
+    assert np.all(np.abs(s - ref) <= 3 * np.spacing(np.float32(ref)) + 1e-45)
+    assert s[-5] == np.float32(0.5) and s[-4] == 0.0 and s[-3] == 1.0 and s[-2] == 0.0 and s[-1] == 1.0
+
+
 # --- whole block closed form (crates/models/src/components/sparse_moe/tests/block.rs:4-72)
 
 def test_block_closed_form_individual_and_packed():
