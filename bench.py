@@ -4,19 +4,25 @@ A "step" is one pass of the routed expert FFN (routing, dispatch, gate_up +
 SiLU·mul, down + route weight, rank-ordered combine) over one batch of
 synthetic tokens already resident in HBM.  Default workload: the
 Qwen3-30B-A3B-shaped layer at batch-64 decode; weights
-rotate over several banks so the 256 MB MALL cannot hold the layer.
+rotate over 4 banks so the 256 MB MALL cannot hold the layer.  The default
+run also measures the same layer at 4096-token prefill and
+reports it under "prefill".
 
-Prints ONE JSON line.  `roofline` describes the dominant kernel of the step,
-timed with HIP events on the stream it runs on; `cpu_baseline` is the C
-restatement of the reference's f32 CPU path (the oracle) on a bounded token
-sample, on this host's cores.
+Prints ONE JSON line.  The headline `value` / `ms_per_step` time exactly
+--steps rotating-bank steps after --warmup.  `timing` adds the reference's
+methodology (crates/models/src/components/cuda/fused_moe/validation/timing.rs:
+7 rounds, the first discarded, median): rotating and hot banks, eager launches
+and HIP-graph replays.  `roofline` describes the dominant kernel of the step
+(the fused decode gate_up kernel for decode, the MFMA grouped gate_up for
+prefill), timed alone with HIP events on the stream it runs on;
+`cpu_baseline` is the C restatement of the reference's f32 CPU path (the
+oracle) on a bounded token sample, on this host's cores.
 """
 from __future__ import annotations
 
 import argparse
 import importlib.util
 import json
-import math
 import os
 import statistics
 import sys
@@ -68,6 +74,9 @@ def parse():
     ap.add_argument("--shared-apart", action="store_true",
                     help="run a shared expert with its own launches instead of folded into the routed schedule")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="with the default workload, skip the c3 prefill sub-object")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -184,28 +193,62 @@ class Layer:
             self.tau.ffi.shared_expert_ex(x, gu_s, dn_s, gate, self.out, act, sh, self.out,
                                           weight_layout=lay, residual=residual)
 
+    def decode_path(self):
+        """True when the step takes the fused decode path (its own projection kernels)."""
+        s = self.shape
+        return self.tile_rows == 16 and s.tokens <= 64 and self.experts <= 256 and \
+            s.hidden % 64 == 0 and s.intermediate % 64 == 0
+
     def projection(self, i, which):
+        """One launch of the step's gate_up (0) or down (1) kernel over the live
+        routes / dispatch, on bank i: the fused decode kernels on the decode
+        path, the grouped kernels otherwise."""
         gu, dn = self.banks[i % len(self.banks)]
         s = self.shape
         if which == 0:
             a, w, out = self.data["x"], gu, self.ws["activated"]
         else:
             a, w, out = self.ws["activated"], dn, self.ws["contributions"]
+        if self.decode_path():
+            self.tau.ffi.decode_projection_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, self.experts,
+                                              self.top_k, which, weight_layout=self.layout)
+            return
         self.tau.ffi.grouped_gemm_ex(a, w, self.ws, out, s.tokens, s.hidden, s.intermediate, self.experts, self.top_k,
                                      self.tile_rows, which, weight_layout=self.layout)
 
 
-def time_events(torch, fn, n):
+def time_events(torch, fn, n, offset=0):
     """Average duration (ms) of n back-to-back launches, HIP events on the launch stream."""
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for i in range(n):
-        fn(i)
+        fn(offset + i)
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) / n
+
+
+def rounds_median(torch, fn, n, rounds):
+    """Median over rounds 1.. of the per-round average (round 0 is discarded),
+    the methodology of the reference's fused-MoE timing
+    (crates/models/src/components/cuda/fused_moe/validation/timing.rs:40-74)."""
+    per_round = [time_events(torch, fn, n, offset=r * n) for r in range(rounds)]
+    return statistics.median(per_round[1:]), per_round
+
+
+def graph_of(torch, fn, count):
+    """A HIP graph holding fn(0) .. fn(count - 1) (one eager pass first)."""
+    for i in range(count):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(count):
+            fn(i)
+    torch.cuda.synchronize()
+    return graph
 
 
 def cpu_baseline(layer, seconds):
@@ -213,7 +256,6 @@ def cpu_baseline(layer, seconds):
     sys.path.insert(0, ROOT)
     from oracle import oracle
 
-    torch = layer.torch
     s = layer.shape
     sample = s.tokens if s.tokens <= 64 else 256
     f = lambda t: t.float().cpu().numpy()
@@ -224,7 +266,12 @@ def cpu_baseline(layer, seconds):
     shared = None
     if s.shared_intermediate:
         shared = (f(layer.data["shared_gate_up"]), f(layer.data["shared_down"]), f(layer.data["shared_gate"]))
-    threads = min(16, os.cpu_count() or 1)
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = nproc
+    threads = max(1, min(16, usable))  # a one-GPU box's CPU share
     oracle.set_threads(threads)
     times = []
     t_end = time.perf_counter() + seconds
@@ -240,9 +287,12 @@ def cpu_baseline(layer, seconds):
         "value": sample / med,
         "unit": "tokens/s",
         "cores": threads,
+        "nproc": nproc,
+        "affinity_cpus": usable,
         "kind": "port",
-        "sample": f"{sample} of {s.tokens} tokens of {s.name}, f32 C restatement (oracle/moe_oracle.c), "
-                  f"median of {len(times) - 1} runs after 1 warm-up",
+        "sample": f"{sample} of {s.tokens} tokens of {s.name}, f32 C restatement of the reference CPU path "
+                  f"(oracle/moe_oracle.c, OpenMP, {threads} threads), median of {len(times) - 1} passes after "
+                  f"1 warm-up, {sum(times):.1f} s of CPU work",
     }
 
 
@@ -275,32 +325,19 @@ def copy_calibration(torch):
     print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
 
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: every GPU box in this build has one MI355X and the MoE layer is "
-              "benchmarked per GPU (expert-parallel sharding is a design note only); run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
-    import torch
-
-    if args.copy_calibration:
-        copy_calibration(torch)
-        return
-    tau = load_package()
-    shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
-    if args.tokens:
-        shape = tau.inputs.scaled(shape, args.tokens)
-    weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
-    banks = args.banks or max(1, min(4, math.ceil(2e9 / weight_bytes)))
+def measure(tau, torch, shape, args, banks, steps, warmup, label):
+    """Times one workload: exactly `steps` rotating-bank steps after `warmup`
+    (the headline), then the reference's rounds methodology for rotating and
+    hot banks, eager and graph-replayed, and the dominant projection alone."""
     layer = Layer(tau, torch, shape, banks, args.tile_rows, args.weight_layout, args.with_norm, args.with_router,
                   args.shared_apart)
-
-    for i in range(args.warmup):
+    print(f"[bench] {label}: {shape.name} T={shape.tokens} banks={banks} tile_rows={layer.tile_rows}",
+          file=sys.stderr, flush=True)
+    for i in range(warmup):
         layer.step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_step = time_events(torch, layer.step, args.steps)
+    ms_step = time_events(torch, layer.step, steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
@@ -311,9 +348,25 @@ def main():
     status = int(meta[2 * layer.experts])
     flops, bytes_ = tau.inputs.algorithmic_work(shape, distinct)
 
-    # Per-projection timing over the live dispatch (one untimed launch each
-    # first: the grouped kernels' code objects load on their first launch).
-    n_proj = max(10, args.steps)
+    # Rounds (7, the first discarded, median of the rest) of `n` steps each.
+    rounds, n = 7, max(10, min(steps, 50))
+    hot = lambda i: layer.step(0)
+    timing = {"rounds": rounds, "steps_per_round": n, "discarded_rounds": 1}
+    timing["rotating_eager_ms"], per_round = rounds_median(torch, layer.step, n, rounds)
+    timing["rotating_eager_rounds_ms"] = per_round
+    timing["hot_eager_ms"], _ = rounds_median(torch, hot, n, rounds)
+    if not args.no_graph:
+        g_rot = graph_of(torch, layer.step, len(layer.banks))
+        g_hot = graph_of(torch, hot, 1)
+        timing["rotating_graph_ms"], _ = rounds_median(torch, lambda i: g_rot.replay(), max(1, n // len(layer.banks)),
+                                                       rounds)
+        timing["rotating_graph_ms"] /= len(layer.banks)
+        timing["hot_graph_ms"], _ = rounds_median(torch, lambda i: g_hot.replay(), n, rounds)
+        del g_rot, g_hot
+
+    # Per-projection timing over the live routes / dispatch (one untimed launch
+    # each first: code objects load on their first launch), rotating banks.
+    n_proj = max(10, steps)
     layer.projection(0, 0)
     layer.projection(0, 1)
     torch.cuda.synchronize()
@@ -322,18 +375,46 @@ def main():
     T, H, I, K = shape.tokens, shape.hidden, shape.intermediate, shape.top_k
     A = T * layer.top_k  # assignments per launch (a folded shared expert adds T)
     d_launch = distinct + (1 if layer.folded else 0)
-    decode = layer.tile_rows <= 32
-    if decode:
-        gu_alg = d_launch * 2 * I * H * 2 + T * H * 2 + A * I * 2
-        dn_alg = d_launch * H * I * 2 + A * I * 2 + A * H * 2
-        gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e9, dn_alg / (ms_dn * 1e-3) / 1e9
-        unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
-        traffic_alg = (gu_alg, dn_alg)
+    # Algorithmic bytes and FLOPs per launch of each projection.
+    gu_bytes = d_launch * 2 * I * H * 2 + T * H * 2 + A * I * 2
+    dn_bytes = d_launch * H * I * 2 + A * I * 2 + A * H * 2
+    gu_flops, dn_flops = 2 * A * H * 2 * I, 2 * A * I * H
+    kernels = {}
+    for name, ms, b, f in (("gate_up", ms_gu, gu_bytes, gu_flops), ("down", ms_dn, dn_bytes, dn_flops)):
+        kernels[name] = {"us": ms * 1e3, "algorithmic_bytes": b, "algorithmic_flops": f,
+                         "GB/s": b / (ms * 1e-3) / 1e9, "TFLOP/s": f / (ms * 1e-3) / 1e12,
+                         "hbm_frac": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         "mfma_frac": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+    dominant = "gate_up" if ms_gu >= ms_dn else "down"
+    k = kernels[dominant]
+    # The metric's roofline: HBM bandwidth for decode-sized batches (the
+    # weight-streaming kernels), MFMA peak for prefill; `binding_frac` is the
+    # kernel's max(F / peak, B / BW) / t whichever binds.
+    hbm_bound = layer.tile_rows <= 32
+    t_floor = max(k["algorithmic_bytes"] / (HBM_PEAK_GBS * 1e9),
+                  k["algorithmic_flops"] / (MFMA_BF16_PEAK_TFLOPS * 1e12))
+    layout_name = "frag16" if layer.layout == tau.ffi.WEIGHTS_FRAG16 else "row_major"
+    kernel_name = dominant + ("_fused" if layer.decode_path() else "")
+    traffic = measured_traffic(shape.name, kernel_name, layout_name)
+    ms_dom = k["us"] * 1e-3
+    if hbm_bound:
+        roofline = {"bound": "hbm", "achieved": k["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": k["hbm_frac"]}
     else:
-        gu_alg, dn_alg = 2 * A * H * 2 * I, 2 * A * I * H
-        gu_rate, dn_rate = gu_alg / (ms_gu * 1e-3) / 1e12, dn_alg / (ms_dn * 1e-3) / 1e12
-        unit, peak, bound = "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "mfma"
-        traffic_alg = (gu_alg, dn_alg)
+        roofline = {"bound": "mfma", "achieved": k["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": k["mfma_frac"]}
+    roofline.update({
+        "traffic": traffic, "kernel": kernel_name,
+        "kernel_symbol": ("decode_gemm_kernel" if layer.decode_path() else "mfma_gemm" if layer.tile_rows >= 64
+                          else "stream_gemm_fast"),
+        "kernel_us": k["us"],
+        "binding_frac": t_floor / (k["us"] * 1e-6),
+        "algorithmic_per_launch": {"bytes": k["algorithmic_bytes"], "flops": k["algorithmic_flops"]},
+        # the same kernel against HBM, from its measured bytes (rocprofv3 FETCH/WRITE_SIZE)
+        "traffic_GBs": traffic / ms_dom / 1e9 if traffic else None,
+        "traffic_over_algorithmic": traffic / k["algorithmic_bytes"] if traffic else None,
+        "kernels": kernels,
+    })
     norm_report = None
     if layer.norm is not None:
         # algorithmic bytes: read x and branch, write residual and normalized (BF16), read the weight
@@ -350,28 +431,11 @@ def main():
         torch.cuda.synchronize()
         router_report = {"projection_and_routing_us": time_events(torch, layer.route_from_hidden, n_proj) * 1e3,
                          "projection_us": time_events(torch, layer.project_router, n_proj) * 1e3}
-    dominant = "gate_up" if ms_gu >= ms_dn else "down"
-    achieved = gu_rate if dominant == "gate_up" else dn_rate
-    ms_dom = ms_gu if dominant == "gate_up" else ms_dn
-    layout_name = "frag16" if layer.layout == tau.ffi.WEIGHTS_FRAG16 else "row_major"
-    traffic = measured_traffic(shape.name, dominant, layout_name)
-
-    tokens_per_s = T / (ms_step * 1e-3)
     layer_hbm = bytes_ / (ms_step * 1e-3) / 1e9
     layer_mfma = flops / (ms_step * 1e-3) / 1e12
-    result = {
-        "metric": "MoE-layer tokens/s; % bf16 MFMA peak (prefill), % HBM BW (decode)",
-        "value": tokens_per_s,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+    out = {
         "ms_per_step": ms_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; random router)",
+        "tokens_per_s": T / (ms_step * 1e-3),
         "config": {
             "workload": shape.name, "tokens": T, "hidden": H, "experts": shape.experts, "top_k": K,
             "intermediate": I, "tile_rows": layer.tile_rows, "weight_banks": banks,
@@ -380,27 +444,74 @@ def main():
             "shared_expert": ("folded" if layer.folded else "separate") if shape.shared_intermediate else None,
             "distinct_experts": distinct, "max_rows_per_expert": int(counts.max()), "plan_status": status,
         },
-        "roofline": {
-            "bound": bound, "kernel": dominant, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": traffic,
-            # the same kernel against HBM, from its measured bytes (rocprofv3 FETCH/WRITE_SIZE)
-            "traffic_GBs": traffic / (ms_dom * 1e-3) / 1e9 if traffic else None,
-            "traffic_hbm_frac": traffic / (ms_dom * 1e-3) / 1e9 / HBM_PEAK_GBS if traffic else None,
-            "kernel_ms": {"gate_up": ms_gu, "down": ms_dn},
-            "algorithmic_per_launch": {"gate_up": traffic_alg[0], "down": traffic_alg[1]},
-        },
+        "roofline": roofline,
         "layer_roofline": {
             "hbm_GBs": layer_hbm, "hbm_frac": layer_hbm / HBM_PEAK_GBS,
             "mfma_TFLOPs": layer_mfma, "mfma_frac": layer_mfma / MFMA_BF16_PEAK_TFLOPS,
+            # max(F/peak, B/BW) / t: the fraction of the binding roofline
+            "roofline_frac": max(flops / (MFMA_BF16_PEAK_TFLOPS * 1e12), bytes_ / (HBM_PEAK_GBS * 1e9))
+                             / (ms_step * 1e-3),
             "algorithmic_bytes": bytes_, "algorithmic_flops": flops,
         },
+        "timing": timing,
         "wall_s_timed": wall,
         **({"residual_norm": norm_report} if norm_report else {}),
         **({"router": router_report} if router_report else {}),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(layer, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(layer, args.cpu_seconds)
+    del layer
+    torch.cuda.empty_cache()
+    return out
+
+
+def default_banks(shape, requested):
+    weight_bytes = 3 * shape.hidden * shape.intermediate * 2 * shape.experts
+    # 4 banks where they fit in 20 GB (every BASELINE layer does), far beyond the 256 MB MALL
+    return requested or (4 if 4 * weight_bytes <= 2e10 else 2)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every GPU box in this build has one MI355X and the MoE layer is "
+              "benchmarked per GPU (expert-parallel sharding is a design note only); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
+    tau = load_package()
+    shape = tau.inputs.CONFIGS[WORKLOADS[args.workload]]
+    if args.tokens:
+        shape = tau.inputs.scaled(shape, args.tokens)
+    main_run = measure(tau, torch, shape, args, default_banks(shape, args.banks), args.steps, args.warmup,
+                       args.workload)
+    result = {
+        "metric": "MoE-layer tokens/s; % bf16 MFMA peak (prefill), % HBM BW (decode)",
+        "value": main_run["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_run["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; random router)",
+        **{k: v for k, v in main_run.items() if k not in ("tokens_per_s", "ms_per_step")},
+    }
+    # The prefill headline (c3: Qwen3-30B-A3B at 4096 tokens) in the same run
+    # when the primary workload is the default decode one.
+    if args.workload == "c2" and not args.tokens and not args.no_prefill:
+        pshape = tau.inputs.CONFIGS[WORKLOADS["c3"]]
+        pre = measure(tau, torch, pshape, args, default_banks(pshape, 0), args.steps, args.warmup, "c3 prefill")
+        result["prefill"] = {"value": pre["tokens_per_s"], "unit": "tokens/s", "steps": args.steps,
+                             "warmup": args.warmup, **pre}
     print(json.dumps(result), flush=True)
 
 

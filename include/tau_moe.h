@@ -194,6 +194,21 @@ int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* ro
                                    int intermediate, int experts, int top_k, int tile_rows, int capacity,
                                    int projection, int weight_layout, int* receipt, void* stream);
 
+/* One projection of the fused decode path (tokens <= 64, E <= 256,
+ * tile_rows 16) from existing routes, exactly the launch that
+ * tau_launch_moe_prefill_ex issues for it: projection 0 = gate_up + SiLU·mul
+ * (a = x [T,H], w = gate_up, out = activated [T*K, I], rows by assignment
+ * t*K + r); projection 1 = down + route weight (a = activated, w = down, out =
+ * contributions [T*K, H]) whose extra workgroup builds meta/offsets/slots/tiles
+ * (required for projection 1; capacity as for tile_rows 16).  The reference's
+ * decode projections are `project` in moe_decode_gemm.cu:47-85 (launched per
+ * expert from fused_bf16_moe_decode.cu:56-91); this entry point exists so that
+ * a caller can time or run the decode projections apart. */
+int tau_launch_moe_decode_projection_ex(const void* a, const void* w, float* routes, int* meta, int* offsets,
+                                        int* slots, int* tiles, void* out, int tokens, int hidden, int intermediate,
+                                        int experts, int top_k, int capacity, int projection, int weight_layout,
+                                        int* receipt, void* stream);
+
 /* Always-on shared expert (shared_expert.rs:39-69): dense gated MLP over all
  * tokens with gate_up_s BF16 [2Is,H], down_s BF16 [Is,H]^T = [H,Is], then
  * output = bf16(fma(sigmoid(x . gate_weight), shared, routed)) (gate_weight

@@ -245,18 +245,11 @@ bool decode_path_supported(int tokens, int hidden, int intermediate, int experts
            (weight_layout == kWeightsRowMajor || weight_layout == kWeightsFrag16);
 }
 
-int launch_decode_moe(const void* input, const void* logits, int logits_dtype, const void* gate_up,
-                      const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
-                      void* activated, void* contributions, void* output, int tokens, int hidden,
-                      int intermediate, int experts, int top_k, int capacity, int weight_layout,
-                      const void* residual, int* receipts, hipStream_t s) {
-    if (!decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout)) return kInvalid;
-    int code = 0;
-    if (logits) {  // otherwise the caller's routes (routing fused with the router projection)
-        code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
-        if (code) return code;
-    }
+namespace {
 
+// Plan arguments of the down launch's plan workgroup (built from the routes).
+DispatchArgs decode_plan_args(float* routes, int* meta, int* offsets, int* slots, int* tiles, int tokens,
+                              int experts, int top_k, int capacity) {
     DispatchArgs plan{};
     plan.routes = routes;
     plan.meta = meta;
@@ -271,8 +264,11 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
     int bits = 0;
     while ((1 << bits) < experts) ++bits;
     plan.expert_bits = bits;
-    const size_t plan_lds = sizeof(int) * dispatch_lds_words<256>(experts);
+    return plan;
+}
 
+DecodeArgs decode_gate_up_args(const void* input, const void* gate_up, const float* routes, void* activated,
+                               int tokens, int hidden, int intermediate, int experts, int top_k, int* receipt) {
     DecodeArgs g{};
     g.a = (const uint16_t*)input;
     g.w = (const uint16_t*)gate_up;
@@ -287,38 +283,91 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
     g.ldo = intermediate;
     g.w_expert_stride = (long)2 * intermediate * hidden;
     g.w_up_offset = intermediate;
-    g.receipt = receipts;
-    DecodeArgs d = g;
+    g.receipt = receipt;
+    return g;
+}
+
+DecodeArgs decode_down_args(const void* activated, const void* down, const float* routes, void* contributions,
+                            int tokens, int hidden, int intermediate, int experts, int top_k, int* receipt) {
+    DecodeArgs d{};
     d.a = (const uint16_t*)activated;
     d.w = (const uint16_t*)down;
+    d.routes = routes;
     d.out = contributions;
+    d.tokens = tokens;
+    d.K = top_k;
+    d.E = experts;
     d.n = hidden;
     d.k = intermediate;
     d.lda = intermediate;
     d.ldo = hidden;
     d.w_expert_stride = (long)hidden * intermediate;
     d.w_up_offset = 0;
-    d.receipt = receipts ? receipts + 5 : nullptr;
+    d.receipt = receipt;
+    return d;
+}
 
-    // Column blocks per wave and K batch depth measured on MI355X for these
-    // kernels (frag16 gate_up 2 x 16 columns, 8 x 32 K; down 4 x 16 columns,
-    // 4 x 32 K for K < 1024 (Qwen3-30B-A3B), 2 x 16 columns, 8 x 32 K for
-    // longer rows (Qwen3-235B-A22B)); the plan workgroup of the down launch
-    // has the same 256 threads as the GEMM workgroups.
+// Column blocks per wave and K batch depth measured on MI355X for these
+// kernels (frag16 gate_up 2 x 16 columns, 8 x 32 K; down 4 x 16 columns,
+// 4 x 32 K for K < 1024 (Qwen3-30B-A3B), 2 x 16 columns, 8 x 32 K for
+// longer rows (Qwen3-235B-A22B)); the plan workgroup of the down launch
+// has the same 256 threads as the GEMM workgroups.
+int launch_decode_gate_up(const DecodeArgs& g, int weight_layout, hipStream_t s) {
+    const DispatchArgs none{};
+    if (weight_layout == kWeightsFrag16)
+        return launch_decode_gemm<kEpiSilu, 2, 8, 4, kWeightsFrag16, false>(g, none, 0, s);
+    return launch_decode_gemm<kEpiSilu, 1, 4, 4, kWeightsRowMajor, false>(g, none, 0, s);
+}
+
+int launch_decode_down(const DecodeArgs& d, const DispatchArgs& plan, int weight_layout, hipStream_t s) {
+    const size_t plan_lds = sizeof(int) * dispatch_lds_words<256>(plan.E);
     if (weight_layout == kWeightsFrag16) {
-        code = launch_decode_gemm<kEpiSilu, 2, 8, 4, kWeightsFrag16, false>(g, plan, 0, s);
-        if (code) return code;
-        if (intermediate < 1024)
-            code = launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
-        else
-            code = launch_decode_gemm<kEpiScatterWeighted, 2, 8, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
-    } else {
-        code = launch_decode_gemm<kEpiSilu, 1, 4, 4, kWeightsRowMajor, false>(g, plan, 0, s);
-        if (code) return code;
-        code = launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsRowMajor, true>(d, plan, plan_lds, s);
+        if (d.k < 1024)
+            return launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
+        return launch_decode_gemm<kEpiScatterWeighted, 2, 8, 4, kWeightsFrag16, true>(d, plan, plan_lds, s);
     }
+    return launch_decode_gemm<kEpiScatterWeighted, 4, 4, 4, kWeightsRowMajor, true>(d, plan, plan_lds, s);
+}
+
+}  // namespace
+
+int launch_decode_moe(const void* input, const void* logits, int logits_dtype, const void* gate_up,
+                      const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
+                      void* activated, void* contributions, void* output, int tokens, int hidden,
+                      int intermediate, int experts, int top_k, int capacity, int weight_layout,
+                      const void* residual, int* receipts, hipStream_t s) {
+    if (!decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout)) return kInvalid;
+    int code = 0;
+    if (logits) {  // otherwise the caller's routes (routing fused with the router projection)
+        code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
+        if (code) return code;
+    }
+    const DispatchArgs plan = decode_plan_args(routes, meta, offsets, slots, tiles, tokens, experts, top_k, capacity);
+    const DecodeArgs g = decode_gate_up_args(input, gate_up, routes, activated, tokens, hidden, intermediate, experts,
+                                             top_k, receipts);
+    const DecodeArgs d = decode_down_args(activated, down, routes, contributions, tokens, hidden, intermediate,
+                                          experts, top_k, receipts ? receipts + 5 : nullptr);
+    code = launch_decode_gate_up(g, weight_layout, s);
+    if (code) return code;
+    code = launch_decode_down(d, plan, weight_layout, s);
     if (code) return code;
     return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, residual, s);
+}
+
+int launch_decode_projection(const void* a, const void* w, float* routes, int* meta, int* offsets, int* slots,
+                             int* tiles, void* out, int tokens, int hidden, int intermediate, int experts, int top_k,
+                             int capacity, int projection, int weight_layout, int* receipt, hipStream_t s) {
+    if (!a || !w || !routes || !out || (projection != 0 && projection != 1) ||
+        !decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout))
+        return kInvalid;
+    if (projection == 0)
+        return launch_decode_gate_up(decode_gate_up_args(a, w, routes, out, tokens, hidden, intermediate, experts,
+                                                         top_k, receipt),
+                                     weight_layout, s);
+    if (!meta || !offsets || !slots || !tiles || capacity < capacity_for(tokens, experts, top_k, 16)) return kInvalid;
+    return launch_decode_down(decode_down_args(a, w, routes, out, tokens, hidden, intermediate, experts, top_k, receipt),
+                              decode_plan_args(routes, meta, offsets, slots, tiles, tokens, experts, top_k, capacity),
+                              weight_layout, s);
 }
 
 }  // namespace tau_amd

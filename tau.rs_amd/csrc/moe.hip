@@ -319,6 +319,14 @@ int tau_launch_moe_grouped_gemm_ex(const void* a, const void* w, const float* ro
     return launch_grouped_gemm(d, tile_rows, kADirect, kEpiScatterWeighted, as_stream(stream));
 }
 
+int tau_launch_moe_decode_projection_ex(const void* a, const void* w, float* routes, int* meta, int* offsets,
+                                        int* slots, int* tiles, void* out, int tokens, int hidden, int intermediate,
+                                        int experts, int top_k, int capacity, int projection, int weight_layout,
+                                        int* receipt, void* stream) {
+    return launch_decode_projection(a, w, routes, meta, offsets, slots, tiles, out, tokens, hidden, intermediate,
+                                    experts, top_k, capacity, projection, weight_layout, receipt, as_stream(stream));
+}
+
 int tau_launch_moe_prefill(const void* input, const void* logits, const void* gate_up, const void* down,
                            float* routes, int* meta, int* offsets, int* slots, int* tiles, void* projected,
                            void* activated, void* contributions, void* output, int tokens, int hidden,

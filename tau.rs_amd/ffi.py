@@ -37,6 +37,7 @@ EXPORTS = (
     "tau_launch_moe_prefill_ex",
     "tau_launch_moe_shared_expert_ex",
     "tau_launch_moe_grouped_gemm_ex",
+    "tau_launch_moe_decode_projection_ex",
     "tau_moe_pack_weights",
     "tau_launch_moe_router_ex",
     "tau_launch_moe_router_route_ex",
@@ -103,6 +104,7 @@ def lib():
         "tau_launch_moe_prefill_ex": [p, p, i, p, p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p, p, p],
         "tau_launch_moe_shared_expert_ex": [p] * 8 + [i, i, i, i, p, p],
         "tau_launch_moe_grouped_gemm_ex": [p] * 7 + [i] * 9 + [p, p],
+        "tau_launch_moe_decode_projection_ex": [p] * 8 + [i] * 8 + [p, p],
         "tau_moe_pack_weights": [p, p, i, i, i, p],
         "tau_launch_moe_router_ex": [p, p, p, p, i, i, i, p],
         "tau_launch_moe_router_route_ex": [p, p, p, p, p, i, i, i, i, p],
@@ -215,6 +217,16 @@ def grouped_gemm_ex(a, w, ws, out, tokens, hidden, intermediate, experts, top_k,
         hidden, intermediate, experts, top_k, tile_rows, ws["capacity"], projection, weight_layout, ptr(receipt),
         stream_ptr(stream))
     check(code, "MoE grouped GEMM")
+
+
+def decode_projection_ex(a, w, ws, out, tokens, hidden, intermediate, experts, top_k, projection, receipt=None,
+                         stream=None, weight_layout=WEIGHTS_ROW_MAJOR):
+    """One fused-decode projection over the workspace's routes (tile_rows 16)."""
+    code = lib().tau_launch_moe_decode_projection_ex(
+        ptr(a), ptr(w), ptr(ws["routes"]), ptr(ws["meta"]), ptr(ws["offsets"]), ptr(ws["slots"]), ptr(ws["tiles"]),
+        ptr(out), tokens, hidden, intermediate, experts, top_k, ws["capacity"], projection, weight_layout,
+        ptr(receipt), stream_ptr(stream))
+    check(code, "MoE decode projection")
 
 
 def combine_ex(contributions, output, meta, tokens, hidden, experts, top_k, stream=None, residual=None):

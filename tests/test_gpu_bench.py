@@ -42,8 +42,18 @@ def test_bench_prints_the_contract(args):
     assert d["value"] > 0 and d["ms_per_step"] > 0 and d["n_gpus"] == 1
     rf = d["roofline"]
     assert rf["bound"] in ("hbm", "mfma") and 0 < rf["frac"] < 1
-    if not args:  # the default run carries the CPU baseline
+    if not args:  # the default run: decode headline, c3 prefill sub-object, CPU baselines, timing rounds
         assert d["cpu_baseline"]["value"] > 0 and d["cpu_baseline"]["cores"] >= 1
+        assert d["cpu_baseline"]["nproc"] >= d["cpu_baseline"]["cores"]
+        assert rf["bound"] == "hbm" and rf["kernel"] == "gate_up_fused"
+        assert d["config"]["weight_banks"] >= 4
+        t = d["timing"]
+        assert t["rounds"] == 7 and len(t["rotating_eager_rounds_ms"]) == 7
+        assert t["hot_eager_ms"] > 0 and t["rotating_graph_ms"] > 0 and t["hot_graph_ms"] > 0
+        p = d["prefill"]
+        assert p["config"]["workload"] == "c3_30b_a3b_prefill" and p["config"]["tile_rows"] >= 64
+        assert p["value"] > 0 and p["roofline"]["bound"] in ("hbm", "mfma") and 0 < p["roofline"]["frac"] < 1
+        assert 0 < p["layer_roofline"]["mfma_frac"] < 1 and p["cpu_baseline"]["value"] > 0
 
 
 def test_bench_rejects_more_than_one_gpu():

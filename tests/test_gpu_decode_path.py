@@ -114,3 +114,38 @@ def compare_paths(tau, shape, layer, layout):
     np.testing.assert_array_equal(v["offsets"].cpu().numpy(), offsets.cpu().numpy())
     np.testing.assert_array_equal(v["slots"].cpu().numpy()[:cap], slots.cpu().numpy())
     np.testing.assert_array_equal(v["tiles"].cpu().numpy()[: cap // 16], tiles.cpu().numpy())
+
+
+@pytest.mark.parametrize("layout", ["frag16", "row_major"])
+def test_decode_projection_entry_point_reproduces_the_step(tau, layout):
+    """tau_launch_moe_decode_projection_ex launches exactly the fused decode
+    path's gate_up and down kernels (the bench times them apart): run after a
+    step on the same routes they rewrite activated, contributions and the plan
+    with identical bits."""
+    shape = tau.inputs.CONFIGS["c2_30b_a3b_decode"]
+    say(f"[decode projection] c2 {layout}")
+    layer = tau.inputs.make_layer(shape)
+    cfg = tau.SparseMoeConfig(shape.hidden, shape.intermediate, shape.experts, shape.top_k)
+    runner = tau.MoePrefillRunner(cfg, layer["gate_up"], layer["down"], weight_layout=layout)
+    assert runner.tile_rows_for(shape.tokens) == 16
+    runner.forward(layer["x"], layer["logits"])
+    torch.cuda.synchronize()
+    ws = runner._ws
+    T, H, I, E, K = shape.tokens, shape.hidden, shape.intermediate, shape.experts, shape.top_k
+    act = ws["activated"][: T * K * I].clone()
+    con = ws["contributions"][: T * K * H].clone()
+    plan = {k: ws[k].clone() for k in ("meta", "offsets", "slots", "tiles")}
+    for k in ("activated", "contributions", "meta", "offsets", "slots", "tiles"):
+        ws[k].fill_(-1 if ws[k].dtype == torch.int32 else 7)
+    tau.ffi.decode_projection_ex(layer["x"], runner.gate_up, ws, ws["activated"], T, H, I, E, K, 0,
+                                 weight_layout=runner.layout)
+    tau.ffi.decode_projection_ex(ws["activated"], runner.down, ws, ws["contributions"], T, H, I, E, K, 1,
+                                 weight_layout=runner.layout)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(ws["activated"][: T * K * I]), bits(act))
+    np.testing.assert_array_equal(bits(ws["contributions"][: T * K * H]), bits(con))
+    cap = ws["capacity"]
+    np.testing.assert_array_equal(ws["meta"][: 2 * E + 2].cpu().numpy(), plan["meta"][: 2 * E + 2].cpu().numpy())
+    np.testing.assert_array_equal(ws["offsets"][: E + 1].cpu().numpy(), plan["offsets"][: E + 1].cpu().numpy())
+    np.testing.assert_array_equal(ws["slots"][:cap].cpu().numpy(), plan["slots"][:cap].cpu().numpy())
+    np.testing.assert_array_equal(ws["tiles"][: cap // 16].cpu().numpy(), plan["tiles"][: cap // 16].cpu().numpy())

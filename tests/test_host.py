@@ -53,6 +53,14 @@ def test_launchers_reject_invalid_arguments_without_a_device(tau):
     assert L.tau_launch_moe_routing_ex(dummy, 1, dummy, 4, 8, 9, null) == 1     # K > E
     assert L.tau_launch_moe_prefill_dispatch(dummy, dummy, dummy, dummy, dummy, 4, 127, 16, null) == 1  # capacity
     assert L.tau_moe_prefill_capacity(1, 256, 8, 48) == -1
+    # routing flags: only TAU_MOE_ROUTE_RAW_WEIGHTS may be OR-ed into the dtype
+    assert L.tau_launch_moe_routing_ex(dummy, 1 | 0x200, dummy, 4, 128, 8, null) == 1
+    assert L.tau_launch_moe_routing_ex(dummy, 2 | 0x100, dummy, 4, 128, 8, null) == 1
+    # decode projections: tokens <= 64, E <= 256, plan buffers for the down projection
+    assert L.tau_launch_moe_decode_projection_ex(*([dummy] * 8), 65, 2048, 768, 128, 8, 4096, 0, 1, null, null) == 1
+    assert L.tau_launch_moe_decode_projection_ex(*([dummy] * 8), 64, 2048, 768, 512, 8, 4096, 0, 1, null, null) == 1
+    assert L.tau_launch_moe_decode_projection_ex(dummy, dummy, dummy, null, null, null, null, dummy,
+                                                 64, 2048, 768, 128, 8, 4096, 1, 1, null, null) == 1
 
 
 def test_sparse_moe_config_validation_messages(tau):
