@@ -24,6 +24,7 @@
 // number of live M blocks is read on the device from the dispatch metadata,
 // so no host readback is needed and dead capacity costs one early exit.
 #include "kernels.hpp"
+#include "mfma_copy_plan.hpp"
 
 namespace tau_amd {
 
@@ -625,11 +626,10 @@ __device__ __forceinline__ void lds_dma16_off(const uint16_t* base, uint32_t off
     typedef __attribute__((address_space(3))) uint16_t* lds_u16;
     const uint32_t lbase = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u16)lds);
     const uint64_t g = (uint64_t)(uintptr_t)base;
-    // readfirstlane returns int: go through uint32_t so the low word is not
-    // sign-extended into the high one.
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
-    const uint64_t gs = ((uint64_t)hi << 32) | (uint64_t)lo;
+    // readfirstlane returns int: the words go back through uint32_t.
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane(address_hi(g));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane(address_lo(g));
+    const uint64_t gs = join_address(hi, lo);
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off_bytes), "s"(gs), "s"(lbase)
                  : "memory", "m0");
 }
@@ -639,18 +639,6 @@ __device__ __forceinline__ void lds_dma16_off(const uint16_t* base, uint32_t off
 // order LDS themselves: copies by wait_vmcnt, fragment reads are consumed by
 // MFMAs (lgkmcnt) before the barrier that lets a stage be overwritten.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// XOR swizzle of the 16-byte chunk slot within a staged row.  LDS has 64
-// banks of 4 bytes (256 bytes); a 16-lane phase of a fragment read touches 16
-// consecutive rows at one chunk, so (row bank offset, swizzled slot) must be
-// distinct over any 16 consecutive rows: 128-byte rows (BK=64) alternate two
-// bank offsets, so the key is (row >> 1) & 7; 64-byte rows (BK=32) cycle four
-// offsets, so the key is (row >> 2) & 3.
-template <int CPR>
-__device__ __forceinline__ int swz(int row) {
-    if constexpr (CPR == 8) return (row >> 1) & 7;
-    else return (row >> 2) & 3;
-}
 
 // IG >= 0 asks the compiler's instruction-group scheduler for strategy IG
 // (__builtin_amdgcn_iglp_opt) in the K loop; 1 interleaves the fragment reads
@@ -758,13 +746,12 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     // Per-lane load sources.  Instruction i of wave w fills rows
     // [q*RPI, (q+1)*RPI) with q = i*(NT/64) + w; lane l supplies row
     // q*RPI + l/CPR into chunk slot l%CPR, i.e. global chunk slot ^ swz(row).
-    const int lrow8 = lane / CPR;
     const uint16_t* a_src[ACH];
     uint32_t a_off[ACH];  // the same as byte offsets from p.a (big wave tiles)
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-        const int r = (i * (NT / 64) + wave) * RPI + lrow8;
-        const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
+        int r, kchunk;
+        row_copy_slot<NT, CPR>(i, wave, lane, r, kchunk);
         long src_row;
         if constexpr (AM == kAGather) {
             const long s_ = row_src[r];
@@ -776,16 +763,6 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         a_off[i] = (uint32_t)((src_row * (long)p.lda + kchunk) * 2);
     }
     const uint16_t* wexp = p.w + (long)expert * p.w_expert_stride;
-    // Weight row of the B tile's row r (gate rows first, then up rows, for SiLU).
-    auto weight_row = [&](int r) -> long {
-        if constexpr (EPI == kEpiSilu) {
-            const int j = c0 + (r < BN / 2 ? r : r - BN / 2);
-            return j < p.n ? (r < BN / 2 ? j : j + p.w_up_offset) : 0;
-        } else {
-            const int j = c0 + r;
-            return j < p.n ? j : 0;
-        }
-    };
     // Row-major weights: staged like A (swizzled 128-byte rows).  Frag16
     // weights: instruction q copies one whole 1 KB fragment (16 rows x 32 of
     // K), so the B stage holds BN/16 bands x BK/32 fragments in global order.
@@ -793,16 +770,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     uint32_t b_off[BCH];  // the same as byte offsets from wexp (big wave tiles)
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
-        const int q = i * (NT / 64) + wave;
-        long e_off;
-        if constexpr (WL == kWeightsFrag16) {
-            const int band = q / (BK / 32), c = q % (BK / 32);
-            e_off = (weight_row(band * 16) >> 4) * 16L * p.k + c * 512 + lane * 8;
-        } else {
-            const int r = q * RPI + lrow8;
-            const int kchunk = ((lane % CPR) ^ swz<CPR>(r)) * 8;
-            e_off = weight_row(r) * (long)p.k + kchunk;
-        }
+        const long e_off = b_copy_offset<NT, CPR, BN, BK, EPI == kEpiSilu, WL == kWeightsFrag16>(
+            i, wave, lane, c0, p.n, p.w_up_offset, p.k);
         b_src[i] = wexp + e_off;
         b_off[i] = (uint32_t)(e_off * 2);
     }

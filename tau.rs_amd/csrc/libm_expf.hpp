@@ -26,11 +26,7 @@
 #pragma once
 #include <stdint.h>
 
-#if defined(__HIPCC__)
-#define TAU_HOST_DEVICE __host__ __device__
-#else
-#define TAU_HOST_DEVICE
-#endif
+#include "host_device.hpp"
 
 namespace tau_amd {
 
