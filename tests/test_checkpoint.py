@@ -1,5 +1,5 @@
 """Checkpoint loading of one sparse-MoE layer (host side; the GPU test is in
-test_gpu_checkpoint.py).  Synthetic checkpoints in both of the reference's
+test_gpu_08_checkpoint.py).  Synthetic checkpoints in both of the reference's
 expert layouts (tensors.rs:37-110) must assemble the same packed tensors, and
 contract violations must name the offending tensor."""
 import pytest
