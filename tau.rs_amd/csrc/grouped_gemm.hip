@@ -640,6 +640,15 @@ __device__ __forceinline__ void lds_dma16_off(const uint16_t* base, uint32_t off
 // MFMAs (lgkmcnt) before the barrier that lets a stage be overwritten.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// -DTAU_SPLIT_ROWS=64|128: 256-row dispatch blocks with at most that many live
+// rows run on the 64x256 (or 128x128) tile in a second launch (default off).
+#ifdef TAU_SPLIT_ROWS
+constexpr int kSplitRows = TAU_SPLIT_ROWS;
+static_assert(kSplitRows == 64 || kSplitRows == 128, "TAU_SPLIT_ROWS is 64 or 128");
+#else
+constexpr int kSplitRows = 0;
+#endif
+
 // IG >= 0 asks the compiler's instruction-group scheduler for strategy IG
 // (__builtin_amdgcn_iglp_opt) in the K loop; 1 interleaves the fragment reads
 // with the MFMAs of a single wave and was measured faster for the 256x256 and
@@ -678,19 +687,31 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
         p.receipt[0] = BM; p.receipt[1] = BN; p.receipt[2] = BK; p.receipt[3] = WM * WN; p.receipt[4] = STAGES;
     }
     const int n_tiles = (p.n + NOUT - 1) / NOUT;
-    const int live = live_blocks(p, BM);
+    // Rows between dispatch blocks: a kernel shorter than 256 rows may run the
+    // small blocks of a 256-row dispatch (small-block split).
+    constexpr bool kStrided = kSplitRows > 0 && BM < 256;
+    const int stride = kStrided && p.block_stride ? p.block_stride : BM;
+    const int live = live_blocks(p, stride);
     const int total = live * n_tiles;
     const int per_xcd = (total + kXcds - 1) / kXcds;
     const int item = xcd_remap(blockIdx.x, per_xcd);
     if (item < 0 || item >= total) return;
     const int m_tile = item / n_tiles, n_tile = item - m_tile * n_tiles;
     const int expert = p.tiles ? p.tiles[m_tile] : 0;
-    const int row0 = m_tile * BM;
+    const int row0 = m_tile * stride;
     const int c0 = n_tile * NOUT;
+    if (kSplitRows > 0 && p.split_rows > 0) {
+        // Padding is a suffix of an expert's block: the block has more than
+        // split_rows live rows iff row row0 + split_rows holds an assignment.
+        const int probe = row0 + p.split_rows;
+        const bool big = probe < p.rows && probe < row0 + stride && p.slots[probe] >= 0 &&
+                         p.slots[probe] < p.assignments;
+        if (BM > p.split_rows ? !big : big) return;  // dead capacity goes to the shorter tile
+    }
     if (expert < 0) {
         if constexpr (EPI == kEpiStoreBf16) {  // dead capacity reads as zeros
             uint16_t* out = (uint16_t*)p.out;
-            for (int i = tid; i < BM * NOUT; i += NT) {
+            for (int i = tid; i < stride * NOUT; i += NT) {
                 const int r = row0 + i / NOUT, c = c0 + i % NOUT;
                 if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
             }
@@ -897,6 +918,17 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
     constexpr int SEGS = NOUT / 8;
     uint16_t* out = (uint16_t*)p.out;
     const bool vec = (p.ldo % 8) == 0 && ((uintptr_t)p.out % 16) == 0;
+    if constexpr (kStrided && EPI != kEpiScatterWeighted) {
+        // A small block run by a kernel shorter than the dispatch block: the
+        // block's rows past BM are padding and are written as zeros.
+        for (int i = tid; i < (stride - BM) * SEGS; i += NT) {
+            const int row = row0 + BM + i / SEGS, col = c0 + (i % SEGS) * 8;
+            if (row >= p.rows || col >= p.n) continue;
+            uint16_t* o = out + (long)row * p.ldo + col;
+            if (vec && col + 8 <= p.n) *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
+            else for (int e = 0; e < 8 && col + e < p.n; ++e) o[e] = 0;
+        }
+    }
     for (int i = tid; i < BM * SEGS; i += NT) {
         const int r = i / SEGS, sg = i - r * SEGS;
         const int row = row0 + r;
@@ -932,7 +964,9 @@ int launch_mfma(const GemmArgs& p, hipStream_t s) {
         const long a_rows = AM == kAGather ? (long)p.assignments / p.topk : (long)p.rows;
         if (a_rows * (long)p.lda * 2 >= (1L << 32) || p.w_expert_stride * 2 >= (1L << 32)) return kInvalid;
     }
-    const long m_blocks = (p.rows + BM - 1) / BM;
+    const int stride = p.block_stride ? p.block_stride : BM;
+    if (stride < BM || stride % BM) return kInvalid;
+    const long m_blocks = (p.rows + stride - 1) / stride;
     const long n_tiles = (p.n + NOUT - 1) / NOUT;
     const long grid = (m_blocks * n_tiles + kXcds - 1) / kXcds * kXcds;
     if (grid <= 0 || grid > 0x7fffffffL) return kInvalid;
@@ -997,6 +1031,7 @@ constexpr int kM256WavesM = 2, kM256WavesN = 2;
 #else
 constexpr int kM256WavesM = 4, kM256WavesN = 4;
 #endif
+
 template <int AM, int EPI, int WL>
 int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
     const bool mfma_ok = aligned && p.k % 64 == 0 && EPI != kEpiStoreF32;
@@ -1005,7 +1040,22 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
             switch (bm) {
                 case 64: return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(p, s);
                 case 128: return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL, 1>(p, s);
-                case 256: return launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(p, s);
+                case 256: {
+                    if constexpr (kSplitRows > 0) {
+                        // Blocks with at most kSplitRows live rows (an expert's
+                        // tail or a lightly routed expert) run on the shorter
+                        // tile, the rest on the 256-row tile.
+                        GemmArgs big = p, small = p;
+                        big.split_rows = small.split_rows = kSplitRows;
+                        small.block_stride = 256;
+                        const int code =
+                            launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(big, s);
+                        if (code) return code;
+                        if constexpr (kSplitRows == 64) return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(small, s);
+                        else return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL, 1>(small, s);
+                    }
+                    return launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(p, s);
+                }
                 default: break;
             }
         }

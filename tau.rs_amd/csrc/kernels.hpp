@@ -31,6 +31,12 @@ struct GemmArgs {
     int w_up_offset;          // rows between gate row j and up row j (I)
     int w_layout;             // WeightLayout of w
     int* receipt;             // optional 5 words stamped by the executed kernel
+    // Small-block split (0 = off): the dispatch's row blocks are `block_stride`
+    // rows apart (0 = the kernel's own BM); with split_rows > 0 a kernel whose
+    // BM exceeds split_rows skips blocks with at most split_rows live rows and
+    // a kernel with BM == split_rows takes only those.
+    int block_stride;
+    int split_rows;
 };
 
 int launch_grouped_gemm(const GemmArgs& p, int bm, int a_mode, int epilogue, hipStream_t s);

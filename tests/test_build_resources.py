@@ -37,7 +37,8 @@ def kernel_resources(tmp_path, defines):
     return out
 
 
-@pytest.mark.parametrize("defines", [[], ["-DTAU_M256_BIG_WAVES"]], ids=["default", "big_waves"])
+@pytest.mark.parametrize("defines", [[], ["-DTAU_M256_BIG_WAVES"], ["-DTAU_SPLIT_ROWS=64"]],
+                         ids=["default", "big_waves", "split64"])
 def test_mfma_tiles_compile_without_spills(tmp_path, defines):
     res = kernel_resources(tmp_path, defines)
     mfma = {k: v for k, v in res.items() if "mfma_gemm" in k}
@@ -46,7 +47,7 @@ def test_mfma_tiles_compile_without_spills(tmp_path, defines):
         assert r.get("VGPRs Spill", 0) == 0 and r.get("SGPRs Spill", 0) == 0, (name, r)
         assert r.get("ScratchSize [bytes/lane]", 0) == 0, (name, r)
     big = {k: v for k, v in mfma.items() if "mfma_gemmILi256ELi256ELi2ELi2E" in k}
-    if defines:
+    if "-DTAU_M256_BIG_WAVES" in defines:
         assert big, "the 128x128 wave-tile kernels were not instantiated"
         for name, r in big.items():
             assert r["AGPRs"] >= 256, (name, r)  # accumulators in AGPRs
