@@ -338,6 +338,16 @@ int launch_decode_moe(const void* input, const void* logits, int logits_dtype, c
                       const void* residual, int* receipts, hipStream_t s) {
     if (!decode_path_supported(tokens, hidden, intermediate, experts, top_k, 16, weight_layout)) return kInvalid;
     int code = 0;
+#ifdef TAU_DECODE_ONE_LAUNCH
+    code = launch_decode_layer(input, logits, logits_dtype, gate_up, down, routes, meta, offsets, slots, tiles,
+                               activated, contributions, tokens, hidden, intermediate, experts, top_k, capacity,
+                               weight_layout, receipts, s);
+    if (code != kNotApplicable) {
+        if (code) return code;
+        return launch_combine(contributions, output, meta + 2 * experts, tokens, hidden, top_k, residual, s);
+    }
+    code = 0;
+#endif
     if (logits) {  // otherwise the caller's routes (routing fused with the router projection)
         code = launch_routing(logits, logits_dtype, routes, tokens, experts, top_k, s);
         if (code) return code;

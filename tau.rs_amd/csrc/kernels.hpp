@@ -62,6 +62,12 @@ int launch_combine(const void* contributions, void* output, const int* status, i
 // path.  Activated/contributions rows are indexed by assignment t*K + r.
 bool decode_path_supported(int tokens, int hidden, int intermediate, int experts, int top_k, int tile_rows,
                            int weight_layout);
+// Returned by optional paths that do not apply to a shape (the caller falls back).
+constexpr int kNotApplicable = -2;
+int launch_decode_layer(const void* input, const void* logits, int logits_dtype, const void* gate_up,
+                        const void* down, float* routes, int* meta, int* offsets, int* slots, int* tiles,
+                        void* activated, void* contributions, int tokens, int hidden, int intermediate, int experts,
+                        int top_k, int capacity, int weight_layout, int* receipts, hipStream_t s);
 int launch_decode_projection(const void* a, const void* w, float* routes, int* meta, int* offsets, int* slots,
                              int* tiles, void* out, int tokens, int hidden, int intermediate, int experts, int top_k,
                              int capacity, int projection, int weight_layout, int* receipt, hipStream_t s);
