@@ -13,8 +13,10 @@
 // E * S workgroups, one per CU, every CU streams the same number of weight
 // bytes (balanced whatever the routing), and the S workgroups of an expert run
 // side by side on one XCD, so the gate_up panel they all read comes from HBM
-// once.  One extra workgroup routes into the API's routes buffer and builds
-// the dispatch plan (meta, offsets, slots, tiles), as in the two-launch path.
+// once.  The workgroups also write the dispatch plan the API returns (meta,
+// offsets, slots, tiles; the two-launch path builds it in one extra
+// workgroup): each counts every assignment (a 2K-entry LDS histogram), and
+// split 0 of expert e writes e's share.
 //
 // Per output element the MFMA sequence (16x16x32 over K in order) and the
 // epilogue roundings are those of the two-launch path, so results are
@@ -34,6 +36,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8_l(u32x4 v) { return __builtin_bit_ca
 constexpr int kLayerWaves = 4;  // one wave per SIMD: the gate_up stream holds ~400 registers
 constexpr int kLayerThreads = 64 * kLayerWaves;
 constexpr int kLayerMaxTokens = 64;
+constexpr int kLayerMaxExperts = 256;
 
 struct DecodeLayerArgs {
     const void* logits;
@@ -170,7 +173,7 @@ __device__ __forceinline__ void stream_columns(const uint16_t* wexp, int n, int 
 // and routes), 16-byte aligned; the layout is spelled out in the kernel.
 __host__ __device__ inline size_t layer_act_offset(int T, int K) {
     const size_t head = 4 * sizeof(int) + kLayerMaxTokens * (sizeof(int) + sizeof(float)) +
-                        (size_t)T * 2 * K * sizeof(float);
+                        kLayerMaxExperts * sizeof(int) + (size_t)T * 2 * K * sizeof(float);
     return (head + 15) / 16 * 16;
 }
 
@@ -178,10 +181,6 @@ __host__ __device__ inline size_t layer_act_offset(int T, int K) {
 template <int EP, typename LT, int NBG, int UG, int NBD, int UD, int WL>
 __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayerArgs p, DispatchArgs plan) {
     extern __shared__ __attribute__((aligned(16))) unsigned char layer_lds[];
-    if (blockIdx.x == gridDim.x - 1) {  // routes into the API buffer + the dispatch plan
-        dispatch_single_body<EP, kLayerThreads>(plan, (int*)layer_lds);
-        return;
-    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int items = p.E * p.splits;
     const int per_xcd = (items + kXcds - 1) / kXcds;
@@ -195,12 +194,14 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
         p.receipt[9] = 1;
     }
     const int T = p.tokens, K = p.K, I = p.I, H = p.H;
-    // LDS: [0] row count; row list [64]; route weights [64]; routes [T][2K]
-    // f32; activated [64][I] bf16 (16-byte aligned).
+    // LDS: [0] row count, [1] rejected-row flag, [2] padded offset of e,
+    // [3] padded total; row list [64]; route weights [64]; per-expert counts
+    // [256]; routes [T][2K] f32; activated [T][I] bf16 (16-byte aligned).
     int* n_rows_lds = (int*)layer_lds;
     int* list = n_rows_lds + 4;
     float* wts = (float*)(list + kLayerMaxTokens);
-    float* routes = wts + kLayerMaxTokens;
+    int* counts = (int*)(wts + kLayerMaxTokens);
+    float* routes = (float*)(counts + kLayerMaxExperts);
     uint16_t* act = (uint16_t*)(layer_lds + layer_act_offset(T, K));
 
     const uint16_t* wgu = p.gate_up + (long)e * 2 * I * H;
@@ -211,15 +212,45 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
 
     LayerBatch<NBG, UG, true> bg;
     // Route every token (four per wave per pass) into LDS.
+    for (int i = tid; i < kLayerMaxExperts; i += kLayerThreads) counts[i] = 0;
+    if (tid == 0) n_rows_lds[1] = 0;
     for (int t0 = 0; t0 < T; t0 += kLayerThreads / 16) {
         const int t = t0 + (tid >> 4);
-        route_row<EP, LT>((const LT*)p.logits, t, t < T, routes, p.E, K, nullptr, p.normalize != 0);
+        if (route_row<EP, LT>((const LT*)p.logits, t, t < T, routes, p.E, K, nullptr, p.normalize != 0) &&
+            t < T)
+            n_rows_lds[1] = 1;  // a rejected row (non-finite logits): the plan is invalid
     }
     __syncthreads();
+    // The dispatch plan (what dispatch_single_body builds for the two-launch
+    // path): every workgroup counts all assignments; split 0 of each expert
+    // writes that expert's counts, offset, slots and tiles, item 0 the
+    // routes, the status and padded total and the tail past the total.
+    const int A = T * K;
+    for (int a = tid; a < A; a += kLayerThreads) {
+        const float id = routes[(a / K) * 2 * K + a % K];
+        if (id == id) atomicAdd(&counts[(int)id], 1);  // NaN ids (rejected rows) count nowhere
+    }
+    __syncthreads();
+    if (wave == 0) {  // padded exclusive offset of e and the padded total
+        int before = 0, total = 0;
+        for (int x = lane; x < p.E; x += 64) {
+            const int pad = (counts[x] + 15) / 16 * 16;
+            before += x < e ? pad : 0;
+            total += pad;
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            before += __shfl_xor(before, d, 64);
+            total += __shfl_xor(total, d, 64);
+        }
+        if (lane == 0) {
+            n_rows_lds[2] = before;
+            n_rows_lds[3] = total;
+        }
+    }
     // This expert's assignments in ascending order (the plan's stable order)
     // and their route weights; a rejected row's ids are NaN and match nothing.
     if (wave == 0) {
-        const int A = T * K;
         int n = 0;
         const float fe = (float)e;
         for (int a0 = 0; a0 < A; a0 += 64) {
@@ -238,6 +269,27 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
     }
     __syncthreads();
     const int n_rows = n_rows_lds[0];
+    if (s == 0) {
+        const int off = n_rows_lds[2], cnt = counts[e], end = off + (cnt + 15) / 16 * 16;
+        if (tid == 0) {
+            plan.meta[e] = cnt;
+            plan.meta[p.E + e] = cnt;
+            plan.offsets[e] = off;
+        }
+        for (int r = tid; r < end - off; r += kLayerThreads) plan.slots[off + r] = r < cnt ? list[r] : A;
+        for (int b = tid; b < (end - off) / 16; b += kLayerThreads) plan.tiles[off / 16 + b] = e;
+    }
+    if (item == 0) {
+        const int total = n_rows_lds[3];
+        if (tid == 0) {
+            plan.offsets[p.E] = total;
+            plan.meta[2 * p.E] = n_rows_lds[1];
+            plan.meta[2 * p.E + 1] = total;
+        }
+        for (int i = tid; i < T * 2 * K; i += kLayerThreads) plan.routes[i] = routes[i];
+        for (int b = total / 16 + tid; b < plan.capacity / 16; b += kLayerThreads) plan.tiles[b] = -1;
+        for (int r = total + tid; r < plan.capacity; r += kLayerThreads) plan.slots[r] = A;
+    }
 
     // gate_up + SiLU·mul into LDS (and, for split 0, the API's activated rows).
     const bool write_global = s == 0;
@@ -308,9 +360,7 @@ int launch_decode_layer(const void* input, const void* logits, int logits_dtype,
     // columns a whole number of 64-column groups.
     int splits = 1;
     while (experts * splits * 2 <= 256 && hidden % (64 * splits * 2) == 0) splits *= 2;
-    const size_t expert_lds = layer_act_offset(tokens, top_k) + (size_t)tokens * intermediate * 2;
-    const size_t plan_lds = sizeof(int) * dispatch_lds_words<kLayerThreads>(experts);
-    const size_t lds = expert_lds > plan_lds ? expert_lds : plan_lds;
+    const size_t lds = layer_act_offset(tokens, top_k) + (size_t)tokens * intermediate * 2;
     if (lds > 150 * 1024 || hidden % 64 || intermediate % 64) return kNotApplicable;
 
     DecodeLayerArgs a{};
@@ -347,7 +397,7 @@ int launch_decode_layer(const void* input, const void* logits, int logits_dtype,
     while ((1 << bits) < experts) ++bits;
     plan.expert_bits = bits;
     const int items = experts * splits;
-    const int grid = (items + kXcds - 1) / kXcds * kXcds + 1;  // + the plan workgroup
+    const int grid = (items + kXcds - 1) / kXcds * kXcds;
     const bool bf = a.logits_bf16;
     if (weight_layout == kWeightsFrag16)
         return bf ? launch_layer_lt<uint16_t, kWeightsFrag16>(a, plan, grid, lds, s)
