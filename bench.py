@@ -511,7 +511,7 @@ def main():
         pshape = tau.inputs.CONFIGS[WORKLOADS["c3"]]
         pre = measure(tau, torch, pshape, args, default_banks(pshape, 0), args.steps, args.warmup, "c3 prefill")
         result["prefill"] = {"value": pre["tokens_per_s"], "unit": "tokens/s", "steps": args.steps,
-                             "warmup": args.warmup, **pre}
+                             "warmup": args.warmup, **{k: v for k, v in pre.items() if k != "tokens_per_s"}}
     print(json.dumps(result), flush=True)
 
 
