@@ -169,6 +169,92 @@ __device__ __forceinline__ void stream_columns(const uint16_t* wexp, int n, int 
     }
 }
 
+// All of one wave's column groups (col0 = first + g * stride, g < groups) as
+// one continuous software pipeline when the expert has at most 16 rows (the
+// usual decode case) and k is a whole number of batches: the next batch's
+// loads are issued before the current batch's MFMAs also across group
+// boundaries, so a wave (one per SIMD here) never waits for a group's first
+// batch.  Otherwise the groups run one by one (stream_columns).  Same MFMA
+// sequence per output element either way.
+template <int NB, int U, int WL, bool SILU, typename ARow, typename Store>
+__device__ __forceinline__ void stream_wave_groups(const uint16_t* wexp, int n, int k, long up_rows, int first,
+                                                   int stride, int groups, const int* list, int n_rows, ARow a_of,
+                                                   Store store) {
+    constexpr int KS = WL == kWeightsFrag16 ? 16 : 1;
+    constexpr int KB = 32 * U;
+    LayerBatch<NB, U, SILU> b0, b1;
+    if (groups <= 0 || n_rows <= 0) return;
+    if (n_rows > 16 || k % KB != 0) {
+        for (int g = 0; g < groups; ++g)
+            stream_columns<NB, U, WL, SILU>(wexp, n, k, up_rows, first + g * stride, list, n_rows, a_of, store, b0,
+                                            false);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const bool ok = (lane & 15) < n_rows;
+    const uint16_t* xs = a_of(ok ? (lane & 15) : 0) + (lane >> 4) * 8;
+    const long up = up_rows * k;
+    const int spg = k / KB;  // batches per group
+    const int total = groups * spg;
+    auto load = [&](LayerBatch<NB, U, SILU>& t, int step) {
+        const int g = step / spg, kb = (step - g * spg) * KB;
+        const int col0 = first + g * stride;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int col = col0 + b * 16 + (lane & 15);
+            const uint16_t* w = WL == kWeightsFrag16 ? wexp + (long)(col < n ? col >> 4 : 0) * 16 * k + lane * 8
+                                                     : wexp + (long)(col < n ? col : 0) * k + (lane >> 4) * 8;
+#pragma unroll
+            for (int q = 0; q < U; ++q) {
+                t.g[b][q] = *(const u32x4*)(w + (kb + q * 32) * KS);
+                if constexpr (SILU) t.u[b][q] = *(const u32x4*)(w + up + (kb + q * 32) * KS);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) t.x[q] = *(const u32x4*)(xs + kb + q * 32);
+    };
+    f32x4 acc_g[NB], acc_u[NB];
+    auto mma = [&](LayerBatch<NB, U, SILU>& t, int step) {
+        const int g = step / spg;
+        if (step == g * spg) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc_g[b][q] = acc_u[b][q] = 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            u32x4 xv = t.x[q];
+            if (!ok) xv = u32x4{0u, 0u, 0u, 0u};
+            const bf16x8 xb = as_bf16x8_l(xv);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                acc_g[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_l(t.g[b][q]), xb, acc_g[b], 0, 0, 0);
+                if constexpr (SILU)
+                    acc_u[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_l(t.u[b][q]), xb, acc_u[b], 0, 0, 0);
+            }
+        }
+        if (step == (g + 1) * spg - 1 && ok) {  // the group's last batch: epilogue
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int oc = first + g * stride + b * 16 + (lane >> 4) * 4;
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    v[q] = SILU ? silu(round_bf16(acc_g[b][q])) * round_bf16(acc_u[b][q]) : acc_g[b][q];
+                store(lane & 15, oc, v);
+            }
+        }
+    };
+    load(b0, 0);
+    for (int step = 0; step < total; step += 2) {
+        if (step + 1 < total) load(b1, step + 1);
+        mma(b0, step);
+        if (step + 2 < total) load(b0, step + 2);
+        if (step + 1 < total) mma(b1, step + 1);
+    }
+}
+
 // Byte offset of the activated rows in LDS (after the count, list, weights
 // and routes), 16-byte aligned; the layout is spelled out in the kernel.
 __host__ __device__ inline size_t layer_act_offset(int T, int K) {
@@ -210,7 +296,6 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
     const int cols_dn = H / p.splits;                    // this split's down columns
     const int ng_dn = (cols_dn + 16 * NBD - 1) / (16 * NBD);
 
-    LayerBatch<NBG, UG, true> bg;
     // Route every token (four per wave per pass) into LDS.
     for (int i = tid; i < kLayerMaxExperts; i += kLayerThreads) counts[i] = 0;
     if (tid == 0) n_rows_lds[1] = 0;
@@ -293,7 +378,7 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
 
     // gate_up + SiLU·mul into LDS (and, for split 0, the API's activated rows).
     const bool write_global = s == 0;
-    for (int cg = wave; cg < ng_gu; cg += kLayerWaves) {
+    {
         auto a_of = [&](int ri) -> const uint16_t* { return p.x + (long)(list[ri] / K) * H; };
         auto store = [&](int ri, int oc, const float* v) {
             u32x2 pk;
@@ -304,14 +389,14 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
                 if (write_global) *(u32x2*)(p.activated + (long)list[ri] * I + oc) = pk;
             }
         };
-        stream_columns<NBG, UG, WL, true>(wgu, I, H, I, cg * 16 * NBG, list, n_rows, a_of, store, bg, false);
+        const int groups = wave < ng_gu ? (ng_gu - wave + kLayerWaves - 1) / kLayerWaves : 0;
+        stream_wave_groups<NBG, UG, WL, true>(wgu, I, H, I, wave * 16 * NBG, kLayerWaves * 16 * NBG, groups, list,
+                                              n_rows, a_of, store);
     }
     __syncthreads();
 
     // down + route weight from the LDS rows, this split's columns.
-    LayerBatch<NBD, UD, false> bd;
-    for (int cg = wave; cg < ng_dn; cg += kLayerWaves) {
-        const int col0 = s * cols_dn + cg * 16 * NBD;
+    {
         auto a_of = [&](int ri) -> const uint16_t* { return act + (long)ri * I; };
         auto store = [&](int ri, int oc, const float* v) {
             const float w = wts[ri];
@@ -320,7 +405,9 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
             pk[1] = pack_bf16x2(v[2] * w, v[3] * w);
             if (oc + 3 < H) *(u32x2*)(p.contributions + (long)list[ri] * H + oc) = pk;
         };
-        stream_columns<NBD, UD, WL, false>(wdn, H, I, 0, col0, list, n_rows, a_of, store, bd, false);
+        const int groups = wave < ng_dn ? (ng_dn - wave + kLayerWaves - 1) / kLayerWaves : 0;
+        stream_wave_groups<NBD, UD, WL, false>(wdn, H, I, 0, s * cols_dn + wave * 16 * NBD, kLayerWaves * 16 * NBD,
+                                               groups, list, n_rows, a_of, store);
     }
 }
 
