@@ -271,9 +271,9 @@ def test_routing_near_max_ulp_ties_f32(tau, oracle, E, K):
 def test_unnormalised_route_weights(tau, oracle, tokens):
     """normalize_selected_weights = false (sparse_moe/config.rs:45,
     routing.rs:198-202): route weights are the selected probabilities; the
-    routing kernel matches the oracle bit for bit and the layer (decode path at
-    16/64 tokens, 128/256-row MFMA path at 256) matches the oracle run with
-    those weights."""
+    routing kernel matches the oracle bit for bit and the layer (fused decode
+    path at 16/64 tokens, the general grouped path at 256) matches the oracle
+    run with those weights."""
     shape = tau.inputs.scaled(tau.inputs.CONFIGS["c3_30b_a3b_prefill"], tokens)
     say(f"[raw weights] T={tokens}")
     layer = tau.inputs.make_layer(shape)
