@@ -176,18 +176,43 @@ __device__ __forceinline__ void stream_columns(const uint16_t* wexp, int n, int 
 // boundaries, so a wave (one per SIMD here) never waits for a group's first
 // batch.  Otherwise the groups run one by one (stream_columns).  Same MFMA
 // sequence per output element either way.
+// Weight part of batch `step` (group step / spg, K batch step % spg): the
+// gate (or only) rows when G, the up rows when UP.
+template <int NB, int U, int WL, bool SILU, bool G = true, bool UP = true>
+__device__ __forceinline__ void load_group_weights(LayerBatch<NB, U, SILU>& t, const uint16_t* wexp, int n, int k,
+                                                   long up, int first, int stride, int spg, int step) {
+    constexpr int KS = WL == kWeightsFrag16 ? 16 : 1;
+    const int lane = threadIdx.x & 63;
+    const int g = step / spg, kb = (step - g * spg) * 32 * U;
+    const int col0 = first + g * stride;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int col = col0 + b * 16 + (lane & 15);
+        const uint16_t* w = WL == kWeightsFrag16 ? wexp + (long)(col < n ? col >> 4 : 0) * 16 * k + lane * 8
+                                                 : wexp + (long)(col < n ? col : 0) * k + (lane >> 4) * 8;
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if constexpr (G) t.g[b][q] = *(const u32x4*)(w + (kb + q * 32) * KS);
+            if constexpr (SILU && UP) t.u[b][q] = *(const u32x4*)(w + up + (kb + q * 32) * KS);
+        }
+    }
+}
+
+// b0: the caller may have issued the gate (or only) rows of batch 0 already
+// (`b0_weights`), e.g. before the rows were known.
 template <int NB, int U, int WL, bool SILU, typename ARow, typename Store>
 __device__ __forceinline__ void stream_wave_groups(const uint16_t* wexp, int n, int k, long up_rows, int first,
                                                    int stride, int groups, const int* list, int n_rows, ARow a_of,
-                                                   Store store) {
-    constexpr int KS = WL == kWeightsFrag16 ? 16 : 1;
+                                                   Store store, LayerBatch<NB, U, SILU>& b0, bool b0_weights) {
     constexpr int KB = 32 * U;
-    LayerBatch<NB, U, SILU> b0, b1;
+    LayerBatch<NB, U, SILU> b1;
     if (groups <= 0 || n_rows <= 0) return;
     if (n_rows > 16 || k % KB != 0) {
-        for (int g = 0; g < groups; ++g)
-            stream_columns<NB, U, WL, SILU>(wexp, n, k, up_rows, first + g * stride, list, n_rows, a_of, store, b0,
+        for (int g = 0; g < groups; ++g) {  // (a gate-only preload of batch 0 is simply loaded again)
+            LayerBatch<NB, U, SILU> t;
+            stream_columns<NB, U, WL, SILU>(wexp, n, k, up_rows, first + g * stride, list, n_rows, a_of, store, t,
                                             false);
+        }
         return;
     }
     const int lane = threadIdx.x & 63;
@@ -196,20 +221,10 @@ __device__ __forceinline__ void stream_wave_groups(const uint16_t* wexp, int n, 
     const long up = up_rows * k;
     const int spg = k / KB;  // batches per group
     const int total = groups * spg;
-    auto load = [&](LayerBatch<NB, U, SILU>& t, int step) {
-        const int g = step / spg, kb = (step - g * spg) * KB;
-        const int col0 = first + g * stride;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int col = col0 + b * 16 + (lane & 15);
-            const uint16_t* w = WL == kWeightsFrag16 ? wexp + (long)(col < n ? col >> 4 : 0) * 16 * k + lane * 8
-                                                     : wexp + (long)(col < n ? col : 0) * k + (lane >> 4) * 8;
-#pragma unroll
-            for (int q = 0; q < U; ++q) {
-                t.g[b][q] = *(const u32x4*)(w + (kb + q * 32) * KS);
-                if constexpr (SILU) t.u[b][q] = *(const u32x4*)(w + up + (kb + q * 32) * KS);
-            }
-        }
+    auto load = [&](LayerBatch<NB, U, SILU>& t, int step, bool gate_loaded) {
+        if (gate_loaded) load_group_weights<NB, U, WL, SILU, false, true>(t, wexp, n, k, up, first, stride, spg, step);
+        else load_group_weights<NB, U, WL, SILU>(t, wexp, n, k, up, first, stride, spg, step);
+        const int kb = (step % spg) * KB;
 #pragma unroll
         for (int q = 0; q < U; ++q) t.x[q] = *(const u32x4*)(xs + kb + q * 32);
     };
@@ -246,11 +261,11 @@ __device__ __forceinline__ void stream_wave_groups(const uint16_t* wexp, int n, 
             }
         }
     };
-    load(b0, 0);
+    load(b0, 0, b0_weights);
     for (int step = 0; step < total; step += 2) {
-        if (step + 1 < total) load(b1, step + 1);
+        if (step + 1 < total) load(b1, step + 1, false);
         mma(b0, step);
-        if (step + 2 < total) load(b0, step + 2);
+        if (step + 2 < total) load(b0, step + 2, false);
         if (step + 1 < total) mma(b1, step + 1);
     }
 }
@@ -296,6 +311,14 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
     const int cols_dn = H / p.splits;                    // this split's down columns
     const int ng_dn = (cols_dn + 16 * NBD - 1) / (16 * NBD);
 
+    // The gate rows of this wave's first gate_up batch are requested before
+    // routing, whose latency they then overlap.
+    // (The launcher requires H to be a whole number of batches, so batch 0
+    // exists; a wave without groups loads column 0's rows and drops them.)
+    const int groups_gu = wave < ng_gu ? (ng_gu - wave + kLayerWaves - 1) / kLayerWaves : 0;
+    LayerBatch<NBG, UG, true> bg;  // gate rows only: the up rows would not fit in registers beside routing
+    load_group_weights<NBG, UG, WL, true, true, false>(bg, wgu, I, H, (long)I * H, wave * 16 * NBG,
+                                                       kLayerWaves * 16 * NBG, H / (32 * UG), 0);
     // Route every token (four per wave per pass) into LDS.
     for (int i = tid; i < kLayerMaxExperts; i += kLayerThreads) counts[i] = 0;
     if (tid == 0) n_rows_lds[1] = 0;
@@ -389,9 +412,8 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
                 if (write_global) *(u32x2*)(p.activated + (long)list[ri] * I + oc) = pk;
             }
         };
-        const int groups = wave < ng_gu ? (ng_gu - wave + kLayerWaves - 1) / kLayerWaves : 0;
-        stream_wave_groups<NBG, UG, WL, true>(wgu, I, H, I, wave * 16 * NBG, kLayerWaves * 16 * NBG, groups, list,
-                                              n_rows, a_of, store);
+        stream_wave_groups<NBG, UG, WL, true>(wgu, I, H, I, wave * 16 * NBG, kLayerWaves * 16 * NBG, groups_gu,
+                                              list, n_rows, a_of, store, bg, true);
     }
     __syncthreads();
 
@@ -406,8 +428,9 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(DecodeLayer
             if (oc + 3 < H) *(u32x2*)(p.contributions + (long)list[ri] * H + oc) = pk;
         };
         const int groups = wave < ng_dn ? (ng_dn - wave + kLayerWaves - 1) / kLayerWaves : 0;
+        LayerBatch<NBD, UD, false> bd;
         stream_wave_groups<NBD, UD, WL, false>(wdn, H, I, 0, s * cols_dn + wave * 16 * NBD, kLayerWaves * 16 * NBD,
-                                               groups, list, n_rows, a_of, store);
+                                               groups, list, n_rows, a_of, store, bd, false);
     }
 }
 
@@ -448,7 +471,8 @@ int launch_decode_layer(const void* input, const void* logits, int logits_dtype,
     int splits = 1;
     while (experts * splits * 2 <= 256 && hidden % (64 * splits * 2) == 0) splits *= 2;
     const size_t lds = layer_act_offset(tokens, top_k) + (size_t)tokens * intermediate * 2;
-    if (lds > 150 * 1024 || hidden % 64 || intermediate % 64) return kNotApplicable;
+    // Whole K batches for both projections (256 = the widest batch, 8 x 32).
+    if (lds > 150 * 1024 || hidden % 256 || intermediate % 256) return kNotApplicable;
 
     DecodeLayerArgs a{};
     a.logits = logits;
