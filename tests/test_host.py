@@ -120,3 +120,22 @@ def test_frag16_entry_points_reject_unsupported_shapes(tau):
     assert L.tau_launch_moe_prefill_ex(d, d, 1, d, d, *args[:8], 64, 128, 128, 8, 2, 16, 4096, 7, None, None,
                                        None) == 1
     assert L.tau_launch_moe_grouped_gemm_ex(*([d] * 7), 64, 96, 128, 8, 2, 16, 4096, 0, 1, None, None) == 1
+
+
+def test_routing_flag_bits_are_validated_on_every_entry_point(tau):
+    """Only TAU_MOE_ROUTE_RAW_WEIGHTS (0x100) may be OR-ed into logits_dtype:
+    any other bit, or a dtype other than 0/1, is rejected before a launch."""
+    L = tau.ffi.lib()
+    d = ctypes.c_void_p(16)
+    for bad in (2, 0x200, 0x101 | 0x400, -1):
+        assert L.tau_launch_moe_routing_ex(d, bad, d, 4, 128, 8, None) == 1
+        assert L.tau_launch_moe_routing_shared_ex(d, bad, d, 4, 128, 8, None) == 1
+        assert L.tau_launch_moe_prefill_dispatch_ex(d, bad, d, d, d, d, d, 4, 128, 8, 16, 4096, None) == 1
+        assert L.tau_launch_moe_prefill_ex(d, d, bad, d, d, *([d] * 8), 64, 2048, 768, 128, 8, 16, 4096, 0, None,
+                                           None, None) == 1
+    assert tau.ffi.ROUTE_RAW_WEIGHTS == 0x100
+
+
+def test_unnormalised_config_is_accepted_by_the_host_mirror(tau):
+    cfg = tau.SparseMoeConfig(64, 64, 8, 2, normalize_selected_weights=False)
+    cfg.validate()  # the reference honours the flag (routing.rs:198-202); so does the HIP path
