@@ -1,10 +1,10 @@
 """The library's routing kernels, run on the CPU under a wavefront emulator,
 against the oracle (CPU; no GPU needed).
 
-tests/wave_emu/route_emu.cpp compiles route_kernel and route_shared_kernel
-from tau.rs_amd/csrc/dispatch.hpp with the host compiler and executes one
-64-lane wavefront at a time, one thread per lane, with the cross-lane
-operations (DPP moves, shuffles) of tests/wave_emu/hip/hip_runtime.h.  This
+tests/wave_emu/route_emu.cpp compiles the routing launchers (routing.hip:
+route_kernel, route_shared_kernel from dispatch.hpp) with the host compiler
+and executes each 64-lane wavefront with one thread per lane and the
+cross-lane operations (DPP moves, shuffles) of tests/wave_emu/hip/hip_runtime.h.  This
 checks the routing algorithm itself (the f32 softmax with glibc's exp bits,
 the denominator summed in expert order, ranking on probabilities with the
 lower id on ties, the rank-ordered renormalisation, the unnormalised and
@@ -12,7 +12,6 @@ shared-expert variants, rejected rows) bit for bit against the oracle's
 restatement of routing.rs:125-257, on the same cases as the GPU tests.  The
 GPU tests (test_gpu_01_parity.py) run the same kernels on the hardware."""
 import os
-import shutil
 import subprocess
 import sys
 
@@ -20,24 +19,22 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CXX = "/opt/rocm/llvm/bin/clang++"
 
 
 @pytest.fixture(scope="module")
 def emu(tmp_path_factory):
-    if not (os.path.exists(CXX) or shutil.which(CXX)):
+    import emu_build
+    if not emu_build.available():
         pytest.skip("clang++ not available")
-    exe = tmp_path_factory.mktemp("emu") / "route_emu"
-    subprocess.run([CXX, "-std=c++20", "-O1", "-pthread", "-I", os.path.join(ROOT, "tests", "wave_emu"),
-                    "-I", os.path.join(ROOT, "tau.rs_amd", "csrc"),
-                    os.path.join(ROOT, "tests", "wave_emu", "route_emu.cpp"), "-o", str(exe)], check=True)
-    work = tmp_path_factory.mktemp("emu_io")
+    work = tmp_path_factory.mktemp("emu")
+    exe = emu_build.build(work, "route_emu.cpp", {"route": (["routing.cpp"], [])})["route"]
 
     def run(logits, k, bf16=False, normalize=True, shared=False):
         lg = np.ascontiguousarray(logits, np.float32)
         t, width = lg.shape
         e = width - (1 if shared else 0)
-        hdr = np.array([t, e, k, int(bf16), int(normalize), int(shared)], np.int32)
+        dtype = (1 if bf16 else 0) | (0 if normalize else 0x100)
+        hdr = np.array([t, e, k, dtype, int(shared)], np.int32)
         if bf16:
             bits = lg.view(np.uint32)
             assert np.all(bits & 0xFFFF == 0), "BF16 logits must be BF16-representable"
@@ -47,7 +44,9 @@ def emu(tmp_path_factory):
         src, dst = work / "in.bin", work / "out.bin"
         src.write_bytes(hdr.tobytes() + payload)
         subprocess.run([str(exe), str(src), str(dst)], check=True, timeout=300)
-        return np.fromfile(dst, np.float32).reshape(t, -1)
+        raw = np.fromfile(dst, np.float32)
+        assert raw[:1].view(np.int32)[0] == 0, "launch status"
+        return raw[1:].reshape(t, -1)
 
     return run
 
