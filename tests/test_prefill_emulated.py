@@ -1,0 +1,141 @@
+"""The whole routed layer through the C ABI (tau_launch_moe_prefill_ex),
+run on the CPU under the wavefront emulator (test infrastructure,
+tests/wave_emu), for the shipped build and the off-by-default tile variants.
+
+tests/wave_emu/prefill_emu.cpp links every library source, rewritten by
+tests/wave_emu/prep.py (the direct-to-LDS copy's inline assembly becomes the
+emulator's copy with the same per-lane source and LDS destination; the
+32x32x16 and 16x16x32 MFMAs are computed in f32), and runs routing, dispatch,
+the grouped MFMA projections and the combine on small layers whose skewed
+routing gives both full and nearly empty 256-row blocks.  Checks:
+  * the shipped build: routes and the dispatch plan equal the oracle's bit
+    for bit, the output is within the BF16 contract's tolerance of the oracle
+    (the emulator's MFMA sums K in order; the hardware's order is not claimed);
+  * -DTAU_M256_BIG_WAVES (2x2 waves of 128x128: 32-bit copy offsets from a
+    scalar base, the variant whose one GPU run faulted) and
+    -DTAU_SPLIT_ROWS=64 / 128 (lightly filled blocks on the shorter tile in a
+    second launch) reproduce the shipped build's activated rows, contributions
+    and output bit for bit: per output element they issue the same MFMA
+    sequence, so any difference is an addressing or scheduling bug."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+torch = pytest.importorskip("torch")
+
+SOURCES = ["combine.cpp", "decode.cpp", "decode_layer.cpp", "decode_moe.cpp", "elementwise.cpp",
+           "grouped_gemm.cpp", "moe.cpp", "norm.cpp", "router.cpp", "routing.cpp"]
+VARIANTS = {"base": [], "bigwaves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"],
+            "split128": ["-DTAU_SPLIT_ROWS=128"]}
+
+
+@pytest.fixture(scope="module")
+def bins(tmp_path_factory):
+    import emu_build
+    if not emu_build.available():
+        pytest.skip("clang++ not available")
+    work = tmp_path_factory.mktemp("prefill_emu")
+    return work, emu_build.build(work, "prefill_emu.cpp", {k: (SOURCES, v) for k, v in VARIANTS.items()})
+
+
+def bf16_bits(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).view(torch.int16).numpy() \
+        .view(np.uint16)
+
+
+def from_bits(b):
+    return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).float().numpy()
+
+
+def run(bins, which, x, logits, gu, dn, K, M, layout, bf16_logits=True):
+    work, exe = bins
+    T, H = x.shape
+    E, two_i, _ = gu.shape
+    I = two_i // 2
+    from frag16_host import frag16_permute
+    gu_b, dn_b = bf16_bits(gu), bf16_bits(dn)
+    if layout == 1:
+        gu_b, dn_b = frag16_permute(gu_b), frag16_permute(dn_b)
+    lg = bf16_bits(logits) if bf16_logits else np.ascontiguousarray(logits, np.float32)
+    hdr = np.array([T, H, I, E, K, M, layout, 1 if bf16_logits else 0], np.int32)
+    src, dst = work / f"in_{which}.bin", work / f"out_{which}.bin"
+    src.write_bytes(hdr.tobytes() + bf16_bits(x).tobytes() + lg.tobytes() + gu_b.tobytes() + dn_b.tobytes())
+    subprocess.run([str(exe[which]), str(src), str(dst)], check=True, timeout=900)
+    raw = np.fromfile(dst, np.uint8)
+    o = 0
+
+    def take(dtype, n):
+        nonlocal o
+        v = raw[o:o + n * np.dtype(dtype).itemsize].view(dtype)
+        o += n * np.dtype(dtype).itemsize
+        return v
+
+    status, cap = take(np.int32, 2)
+    assert status == 0, status
+    return {"routes": take(np.float32, T * 2 * K).reshape(T, 2 * K), "meta": take(np.int32, 2 * E + 2),
+            "offsets": take(np.int32, E + 1), "slots": take(np.int32, cap), "tiles": take(np.int32, cap // M),
+            "activated": take(np.uint16, cap * I).reshape(cap, I), "contributions": take(np.uint16, T * K * H),
+            "output": take(np.uint16, T * H).reshape(T, H), "cap": int(cap)}
+
+
+def layer(seed, T, H, I, E, skew=True):
+    rng = np.random.default_rng(seed)
+    x = from_bits(bf16_bits(rng.standard_normal((T, H))))
+    gu = from_bits(bf16_bits(rng.standard_normal((E, 2 * I, H)) * 0.05))
+    dn = from_bits(bf16_bits(rng.standard_normal((E, H, I)) * 0.05))
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    if skew:  # expert 0 takes most tokens: full 256-row blocks beside nearly empty ones
+        logits[:, 0] += 3.0
+    return x, logits, gu, dn
+
+
+def check_against_oracle(oracle, res, x, logits, gu, dn, K, M, bf16_logits=True):
+    E = gu.shape[0]
+    lg = from_bits(bf16_bits(logits)) if bf16_logits else logits
+    ids, w = oracle.route(lg, K)
+    np.testing.assert_array_equal(res["routes"][:, :K].astype(np.int64), ids)
+    np.testing.assert_array_equal(res["routes"][:, K:], w)
+    meta, offsets, slots, tiles = oracle.dispatch(ids, E, M, res["cap"])
+    np.testing.assert_array_equal(res["meta"], meta)
+    np.testing.assert_array_equal(res["offsets"], offsets)
+    np.testing.assert_array_equal(res["slots"], slots)
+    np.testing.assert_array_equal(res["tiles"], tiles)
+    ref = oracle.moe(x, ids, w, gu, dn, bf16=True)
+    got = from_bits(res["output"])
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err <= 2e-3, err
+    return meta
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+def test_256_row_tiles_and_variants(bins, oracle, layout):
+    T, H, I, E, K = 160, 256, 256, 8, 2
+    x, logits, gu, dn = layer(11 + layout, T, H, I, E)
+    base = run(bins, "base", x, logits, gu, dn, K, 256, layout)
+    meta = check_against_oracle(oracle, base, x, logits, gu, dn, K, 256)
+    counts = meta[:E]
+    assert counts.max() > 128 and (counts[counts > 0] <= 64).any()  # both kinds of block
+    for v in ("bigwaves", "split64", "split128"):
+        res = run(bins, v, x, logits, gu, dn, K, 256, layout)
+        for key in ("routes", "meta", "slots", "tiles", "contributions", "output"):
+            np.testing.assert_array_equal(res[key].view(np.uint32) if res[key].dtype == np.float32 else res[key],
+                                          base[key].view(np.uint32) if base[key].dtype == np.float32 else base[key],
+                                          err_msg=f"{v}: {key}")
+        live = base["slots"] < T * K  # rows holding an assignment (padding and dead rows are layout details)
+        np.testing.assert_array_equal(res["activated"][live], base["activated"][live], err_msg=f"{v}: activated")
+
+
+@pytest.mark.parametrize("M,layout,bf16_logits", [(64, 0, False), (128, 1, True)])
+def test_shorter_tiles(bins, oracle, M, layout, bf16_logits):
+    T, H, I, E, K = 96, 256, 192, 6, 3
+    x, logits, gu, dn = layer(20 + M, T, H, I, E)
+    if layout == 1:  # FRAG16 needs I % 64 == 0
+        x, logits, gu, dn = layer(20 + M, T, H, 256, E)
+    res = run(bins, "base", x, logits, gu, dn, K, M, layout, bf16_logits)
+    check_against_oracle(oracle, res, x, logits, gu, dn, K, M, bf16_logits)

@@ -29,6 +29,7 @@
 #include <functional>
 #include <memory>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 #define __device__
@@ -40,8 +41,9 @@
 struct EmuDim3 {
     unsigned x = 0, y = 0, z = 0;
     EmuDim3() = default;
-    EmuDim3(unsigned v) : x(v) {}
+    EmuDim3(unsigned x_, unsigned y_ = 1, unsigned z_ = 1) : x(x_), y(y_), z(z_) {}
 };
+typedef EmuDim3 dim3;
 // The running work item's coordinates (set by the scheduler before it resumes a work item).
 inline EmuDim3 threadIdx, blockIdx, blockDim, gridDim;
 
@@ -144,9 +146,9 @@ inline void item_entry() {
 }
 
 // Runs grid x block work items, workgroup by workgroup.
-inline void launch(unsigned grid, unsigned block, size_t lds, const std::function<void()>& fn) {
+inline void launch(EmuDim3 grid, unsigned block, size_t lds, const std::function<void()>& fn) {
     constexpr size_t kStack = 128 * 1024;
-    for (unsigned g = 0; g < grid; ++g) {
+    for (unsigned g = 0; g < grid.x * grid.y; ++g) {
         Group grp;
         grp.bar.expected = (int)block;
         grp.waves.resize((block + 63) / 64);
@@ -155,9 +157,9 @@ inline void launch(unsigned grid, unsigned block, size_t lds, const std::functio
         grp.items.resize(block);
         group = &grp;
         body = &fn;
-        blockIdx.x = g;
-        blockDim.x = block;
-        gridDim.x = grid;
+        blockIdx = EmuDim3(g % grid.x, g / grid.x, 0);
+        blockDim = EmuDim3(block);
+        gridDim = grid;
         for (unsigned t = 0; t < block; ++t) {
             Item& it = grp.items[t];
             it.stack.reset(new char[kStack]);
@@ -194,7 +196,8 @@ template <typename F, typename G, typename B, typename... Rest>
 inline void launch_with(F fn, G grid, B block, Rest... rest) {
     size_t lds = 0;
     if constexpr (sizeof...(Rest) >= 1) lds = (size_t)std::get<0>(std::tuple<Rest...>(rest...));
-    launch((unsigned)grid, (unsigned)block, lds, fn);
+    if constexpr (std::is_same_v<G, EmuDim3>) launch(grid, (unsigned)block, lds, fn);
+    else launch(EmuDim3((unsigned)grid), (unsigned)block, lds, fn);
 }
 }  // namespace emu
 
@@ -265,3 +268,42 @@ inline emu_f32x4 emu_mfma_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c)
     return d;
 }
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, x, y, z) emu_mfma_16x16x32_bf16(a, b, c)
+
+// v_mfma_f32_32x32x16_bf16: lane l holds A[l%32][8(l/32)..+8], B[8(l/32)..+8][l%32]
+// and D[8(q/4) + 4(l/32) + q%4][l%32], q = 0..15.
+typedef float emu_f32x16 __attribute__((ext_vector_type(16)));
+inline emu_f32x16 emu_mfma_32x32x16_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x16 c) {
+    emu::Wave& w = emu::wave();
+    const int l = emu::lane();
+    std::memcpy(w.a[l], &a, 16);
+    std::memcpy(w.b[l], &b, 16);
+    emu::arrive(w.bar);
+    emu_f32x16 d = c;
+    const int j = l % 32;
+    for (int q = 0; q < 16; ++q) {
+        const int i = 8 * (q / 4) + 4 * (l / 32) + q % 4;
+        float acc = c[q];
+        for (int k = 0; k < 16; ++k) {
+            const int kq = k / 8, ke = k % 8;
+            __bf16 av, bv;
+            std::memcpy(&av, (const char*)w.a[kq * 32 + i] + 2 * ke, 2);
+            std::memcpy(&bv, (const char*)w.b[kq * 32 + j] + 2 * ke, 2);
+            acc += (float)av * (float)bv;
+        }
+        d[q] = acc;
+    }
+    emu::arrive(w.bar);
+    return d;
+}
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, x, y, z) emu_mfma_32x32x16_bf16(a, b, c)
+#define __builtin_amdgcn_iglp_opt(x) ((void)0)
+#define __builtin_amdgcn_sched_barrier(x) ((void)0)
+
+namespace emu {
+// global_load_lds_dwordx4: each lane copies 16 bytes from its source to the
+// wave's LDS base (the first lane's destination) + 16 * lane.
+inline void dma16(const uint16_t* src, uint16_t* lds) {
+    uint16_t* base = __shfl(lds, 0);
+    std::memcpy(base + 8 * lane(), src, 16);
+}
+}  // namespace emu
