@@ -131,8 +131,10 @@ def test_256_row_tiles_and_variants(bins, oracle, layout):
         np.testing.assert_array_equal(res["activated"][live], base["activated"][live], err_msg=f"{v}: activated")
 
 
-@pytest.mark.parametrize("M,layout,bf16_logits", [(64, 0, False), (128, 1, True)])
+@pytest.mark.parametrize("M,layout,bf16_logits", [(16, 1, True), (32, 0, True), (64, 0, False), (128, 1, True)])
 def test_shorter_tiles(bins, oracle, M, layout, bf16_logits):
+    """16/32-row blocks: the weight-streaming grouped kernels (96 tokens, so not
+    the fused decode path); 64/128: the shorter MFMA tiles."""
     T, H, I, E, K = 96, 256, 192, 6, 3
     x, logits, gu, dn = layer(20 + M, T, H, I, E)
     if layout == 1:  # FRAG16 needs I % 64 == 0
