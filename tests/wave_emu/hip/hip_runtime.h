@@ -51,7 +51,18 @@ typedef int hipError_t;
 typedef void* hipStream_t;
 constexpr int hipSuccess = 0;
 constexpr int hipErrorInvalidValue = 1;
+constexpr int hipErrorInvalidSymbol = 13;
 inline hipError_t hipGetLastError() { return hipSuccess; }
+inline hipError_t hipGetDevice(int* d) {
+    *d = 0;
+    return hipSuccess;
+}
+inline hipError_t hipGetSymbolAddress(void** p, const void* symbol) {
+    *p = const_cast<void*>(symbol);
+    return hipSuccess;
+}
+#define HIP_SYMBOL(x) (&(x))
+#define __align__(n) alignas(n)
 
 inline float __uint_as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
 inline uint32_t __float_as_uint(float f) { return __builtin_bit_cast(uint32_t, f); }
