@@ -136,6 +136,10 @@ __global__ __launch_bounds__(64 * W) void decode_gemm_kernel(DecodeArgs p, Dispa
         }
     }
     if (n_rows > kListRows) n_rows = kListRows;  // unreachable for T <= 64 (one rank per token and expert)
+    // The list is read below by other lanes of this wave: the wave's LDS
+    // stores come first (waves execute in order; this keeps the compiler from
+    // moving the reads above them).
+    __builtin_amdgcn_wave_barrier();
 
     for (int g0 = 0; g0 < n_rows; g0 += 16) {
         const int a_row = list[g0 + (lane & 15)];  // -1: padding lane

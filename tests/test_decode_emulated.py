@@ -86,6 +86,7 @@ CASES = [  # T, H, I, E, K, layout, bf16 logits, raw weights, NaN row
     (5, 256, 512, 16, 4, 0, False, False, False),
     (12, 256, 256, 24, 3, 1, True, True, False),
     (8, 256, 256, 8, 2, 1, True, False, True),
+    (64, 256, 256, 32, 8, 1, True, False, False),  # skewed below: experts with 17-64 rows (row groups 2-4)
 ]
 
 
@@ -101,6 +102,10 @@ def test_decode_path_emulated(bins, oracle, case):
         logits = from_bits(bf16_bits(logits))
     if nan_row:
         logits[3, 1] = np.nan
+    if T == 64:  # a per-expert popularity bias: some experts take most tokens
+        logits = logits + (rng.standard_normal(E) * 1.5).astype(np.float32)
+        if bf16_logits:
+            logits = from_bits(bf16_bits(logits))
     run.K = K
     two = run(bins, "two", x, logits, gu, dn, layout, bf16_logits, raw)
     one = run(bins, "one", x, logits, gu, dn, layout, bf16_logits, raw)
@@ -116,6 +121,8 @@ def test_decode_path_emulated(bins, oracle, case):
     if nan_row:
         assert two["meta"][2 * E] == 1 and np.all(np.isnan(from_bits(two["output"])))
         return
+    if T == 64:
+        assert two["meta"][:E].max() > 32  # several 16-row groups for one expert
     ids, w = oracle.route(logits, K, normalize=not raw)
     np.testing.assert_array_equal(two["routes"][:, :K].astype(np.int64), ids)
     np.testing.assert_array_equal(two["routes"][:, K:], w)

@@ -247,6 +247,10 @@ inline uint64_t __ballot(int pred) {
 }
 inline int __any(int pred) { return __ballot(pred) != 0; }
 inline void __syncthreads() { emu::arrive(emu::group->bar); }
+// On the GPU a wave's lanes run in lockstep, so values a wave stores to LDS
+// are visible to its other lanes' later loads; the emulator's lanes run apart
+// between synchronisation points, and the kernels mark these places.
+#define __builtin_amdgcn_wave_barrier() emu::arrive(emu::wave().bar)
 inline int emu_readlane(int v, int l) { return (int)emu::exchange((uint32_t)v, l, 0); }
 #define __builtin_amdgcn_readlane(v, l) emu_readlane(v, l)
 #define __builtin_amdgcn_readfirstlane(v) emu_readlane(v, 0)
