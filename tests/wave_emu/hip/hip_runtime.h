@@ -2,7 +2,8 @@
 // tests/test_decode_emulated.py): a CPU stand-in for the HIP device
 // environment, large enough to compile the library's routing and decode
 // kernels for the host and run them.  A workgroup's work items are user-level
-// contexts (ucontext) on one thread, switched at barriers; each 64-lane
+// contexts (own stacks, an x86-64 register switch) on one thread, switched at
+// barriers; each 64-lane
 // wavefront exchanges cross-lane values (DPP moves, shuffles, ballots, MFMA
 // operands) through a shared array between two phases of a per-wave barrier,
 // so every lane of a wave must reach them in the same order, as on the GPU,
@@ -18,7 +19,6 @@
 // Sources with <<< >>> launches and __shared__ declarations are rewritten for
 // this header by tests/wave_emu/prep.py.  Never part of the library build.
 #pragma once
-#include <ucontext.h>
 
 #include <cmath>
 #include <cstddef>
@@ -84,8 +84,27 @@ struct Barrier {
     int expected = 0, arrived = 0;
     unsigned generation = 0;
 };
+// x86-64 context switch: saves the callee-saved registers on the current
+// stack, stores the stack pointer in *save, continues on the stack `next`
+// (as left by a previous switch, or prepared by make_stack).
+__attribute__((naked, noinline)) static void switch_stack(void** save, void* next) {
+    asm volatile(
+        "push %rbp\n\tpush %rbx\n\tpush %r12\n\tpush %r13\n\tpush %r14\n\tpush %r15\n\t"
+        "mov %rsp, (%rdi)\n\tmov %rsi, %rsp\n\t"
+        "pop %r15\n\tpop %r14\n\tpop %r13\n\tpop %r12\n\tpop %rbx\n\tpop %rbp\n\tret");
+}
+// A fresh stack whose first switch enters `entry` (which never returns).
+inline void* make_stack(char* base, size_t size, void (*entry)()) {
+    uintptr_t top = ((uintptr_t)base + size) & ~(uintptr_t)15;
+    void** sp = (void**)top;
+    *--sp = nullptr;          // entry's (unused) return address: rsp % 16 == 8 on entry
+    *--sp = (void*)entry;     // popped by the switch's ret
+    for (int i = 0; i < 6; ++i) *--sp = nullptr;  // rbp, rbx, r12-r15
+    return sp;
+}
+
 struct Item {
-    ucontext_t ctx;
+    void* sp = nullptr;
     std::unique_ptr<char[]> stack;
     bool done = false;
     Barrier* waiting = nullptr;  // barrier it waits at
@@ -101,7 +120,7 @@ struct Group {
     std::vector<Wave> waves;
     std::vector<unsigned char> lds;
     std::vector<Item> items;
-    ucontext_t scheduler;
+    void* scheduler_sp = nullptr;
     unsigned current = 0;
 };
 inline Group* group = nullptr;
@@ -118,7 +137,7 @@ inline void arrive(Barrier& b) {
         b.arrived = 0;
         ++b.generation;
     }
-    swapcontext(&me.ctx, &group->scheduler);
+    switch_stack(&me.sp, group->scheduler_sp);
 }
 
 // Publishes v, waits for the wave, returns lane src's value (or `fallback`
@@ -152,8 +171,10 @@ inline int dpp_source(int l, int ctrl) {
 
 inline void item_entry() {
     (*body)();
-    group->items[group->current].done = true;
-    // returning switches to uc_link (the scheduler)
+    Item& me = group->items[group->current];
+    me.done = true;
+    switch_stack(&me.sp, group->scheduler_sp);  // never resumed
+    std::abort();
 }
 
 // Runs grid x block work items, workgroup by workgroup.
@@ -174,11 +195,7 @@ inline void launch(EmuDim3 grid, unsigned block, size_t lds, const std::function
         for (unsigned t = 0; t < block; ++t) {
             Item& it = grp.items[t];
             it.stack.reset(new char[kStack]);
-            getcontext(&it.ctx);
-            it.ctx.uc_stack.ss_sp = it.stack.get();
-            it.ctx.uc_stack.ss_size = kStack;
-            it.ctx.uc_link = &grp.scheduler;
-            makecontext(&it.ctx, item_entry, 0);
+            it.sp = make_stack(it.stack.get(), kStack, item_entry);
         }
         // Round-robin over runnable work items until all have returned.
         for (;;) {
@@ -191,7 +208,7 @@ inline void launch(EmuDim3 grid, unsigned block, size_t lds, const std::function
                 it.waiting = nullptr;
                 grp.current = t;
                 threadIdx.x = t;
-                swapcontext(&grp.scheduler, &it.ctx);
+                switch_stack(&grp.scheduler_sp, it.sp);
                 progressed = true;
             }
             if (all_done) break;
