@@ -141,3 +141,23 @@ def test_shorter_tiles(bins, oracle, M, layout, bf16_logits):
         x, logits, gu, dn = layer(20 + M, T, H, 256, E)
     res = run(bins, "base", x, logits, gu, dn, K, M, layout, bf16_logits)
     check_against_oracle(oracle, res, x, logits, gu, dn, K, M, bf16_logits)
+
+
+@pytest.mark.parametrize("H,I,T", [(2048, 768, 320), (4096, 1536, 272)], ids=["c3_dims", "c5p_dims"])
+def test_benchmark_layer_dims(bins, oracle, H, I, T):
+    """The 256-row MFMA tile at the hidden and intermediate sizes of the
+    30B-A3B (c3) and 235B-A22B (c5 prefill) layers: full-length K loops
+    (32 / 64 steps of 64), the real operand strides, and a skewed expert with
+    one full and one nearly empty block.  Three experts keep the emulated work
+    to a few GFLOP.  The shipped build is checked against the oracle, the
+    128x128 wave-tile build bit for bit against it."""
+    import concurrent.futures
+    E, K = 3, 2
+    x, logits, gu, dn = layer(5, T, H, I, E)
+    with concurrent.futures.ThreadPoolExecutor(2) as ex:
+        futs = {v: ex.submit(run, bins, v, x, logits, gu, dn, K, 256, 1) for v in ("base", "bigwaves")}
+        res = {v: f.result() for v, f in futs.items()}
+    meta = check_against_oracle(oracle, res["base"], x, logits, gu, dn, K, 256)
+    assert meta[0] > 256 and meta[0] % 256 <= 64  # a full block and a nearly empty one
+    for key in ("routes", "slots", "contributions", "output"):
+        np.testing.assert_array_equal(res["bigwaves"][key], res["base"][key], err_msg=key)
