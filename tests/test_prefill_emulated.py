@@ -53,17 +53,20 @@ def from_bits(b):
     return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).float().numpy()
 
 
-def run(bins, which, x, logits, gu, dn, K, M, layout, bf16_logits=True):
+def run(bins, which, x, logits, gu, dn, K, M, layout, bf16_logits=True, shared=0):
+    """shared=1: gu/dn hold the shared expert as expert E and logits its gate
+    column last; the routes then have K+1 picks."""
     work, exe = bins
     T, H = x.shape
     E, two_i, _ = gu.shape
+    E -= shared
     I = two_i // 2
     from frag16_host import frag16_permute
     gu_b, dn_b = bf16_bits(gu), bf16_bits(dn)
     if layout == 1:
         gu_b, dn_b = frag16_permute(gu_b), frag16_permute(dn_b)
     lg = bf16_bits(logits) if bf16_logits else np.ascontiguousarray(logits, np.float32)
-    hdr = np.array([T, H, I, E, K, M, layout, 1 if bf16_logits else 0], np.int32)
+    hdr = np.array([T, H, I, E, K, M, layout, 1 if bf16_logits else 0, shared], np.int32)
     src, dst = work / f"in_{which}.bin", work / f"out_{which}.bin"
     src.write_bytes(hdr.tobytes() + bf16_bits(x).tobytes() + lg.tobytes() + gu_b.tobytes() + dn_b.tobytes())
     subprocess.run([str(exe[which]), str(src), str(dst)], check=True, timeout=900)
@@ -78,6 +81,7 @@ def run(bins, which, x, logits, gu, dn, K, M, layout, bf16_logits=True):
 
     status, cap = take(np.int32, 2)
     assert status == 0, status
+    E, K = E + shared, K + shared
     return {"routes": take(np.float32, T * 2 * K).reshape(T, 2 * K), "meta": take(np.int32, 2 * E + 2),
             "offsets": take(np.int32, E + 1), "slots": take(np.int32, cap), "tiles": take(np.int32, cap // M),
             "activated": take(np.uint16, cap * I).reshape(cap, I), "contributions": take(np.uint16, T * K * H),
@@ -161,3 +165,39 @@ def test_benchmark_layer_dims(bins, oracle, H, I, T):
     assert meta[0] > 256 and meta[0] % 256 <= 64  # a full block and a nearly empty one
     for key in ("routes", "slots", "contributions", "output"):
         np.testing.assert_array_equal(res["bigwaves"][key], res["base"][key], err_msg=key)
+
+
+def test_folded_shared_expert_c4_dims(bins, oracle):
+    """The c4 layer's always-on shared expert folded into the routed schedule
+    (tau_launch_moe_routing_shared_ex, then tau_launch_moe_prefill_ex from the
+    routes with E+1 experts and K+1 picks) at c4's hidden and intermediate
+    sizes (2048, 512), 16 routed experts, top-4, 256 tokens on 256-row tiles
+    (the shared expert fills a whole block).  Routed ranks equal the oracle's
+    routing bit for bit and rank K is (E, sigmoid(gate)); the output is within
+    the BF16 contract's tolerance of the oracle run as E+1 experts, and within
+    the north-star tolerance of the reference's f32 path with the separate
+    shared combine (routed + sigmoid(x . w_s) * mlp_s(x), shared_expert.rs:39-69)."""
+    T, H, I, E, K = 256, 2048, 512, 16, 4
+    x, logits, gu, dn = layer(31, T, H, I, E + 1)
+    rng = np.random.default_rng(32)
+    w_s = rng.standard_normal(H).astype(np.float32) * 0.02
+    logits[:, E] = x @ w_s  # the shared gate logit x . w_s, last column
+    res = run(bins, "base", x, logits, gu, dn, K, 256, 1, bf16_logits=False, shared=1)
+    ids, w = oracle.route(logits[:, :E], K)
+    gate = oracle.sigmoid(logits[:, E])
+    r = res["routes"]
+    np.testing.assert_array_equal(r[:, :K].astype(np.int64), ids)
+    np.testing.assert_array_equal(r[:, K + 1:2 * K + 1], w)
+    assert np.all(r[:, K] == E)
+    np.testing.assert_array_equal(r[:, 2 * K + 1], gate)
+    ids_x = np.concatenate([ids, np.full((T, 1), E, np.int64)], 1)
+    w_x = np.concatenate([w, gate[:, None]], 1).astype(np.float32)
+    meta, offsets, slots, tiles = oracle.dispatch(ids_x, E + 1, 256, res["cap"])
+    np.testing.assert_array_equal(res["meta"], meta)
+    np.testing.assert_array_equal(res["slots"], slots)
+    got = from_bits(res["output"])
+    ref_bf16 = oracle.moe(x, ids_x, w_x, gu, dn, bf16=True)
+    assert np.linalg.norm(got - ref_bf16) / np.linalg.norm(ref_bf16) <= 2e-3
+    routed = oracle.moe(x, ids, w, gu[:E], dn[:E])
+    ref = oracle.shared_combine_f32(x, w_s, oracle.dense_mlp(x, gu[E], dn[E]), routed)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-2

@@ -3,8 +3,12 @@
 // dispatch, the grouped gate_up and down projections, the combine) on the CPU
 // emulator of wave_emu/hip/hip_runtime.h.
 // usage: prefill_emu in.bin out.bin
-//   in.bin:  int32 T, H, I, E, K, tile_rows, weight_layout, logits_dtype; then
-//            x [T,H] u16, logits [T,E] (f32 or u16), gate_up [E,2I,H] u16, down [E,H,I] u16
+//   in.bin:  int32 T, H, I, E, K, tile_rows, weight_layout, logits_dtype, shared; then
+//            x [T,H] u16, logits [T,E'] (f32 or u16), gate_up [E',2I,H] u16, down [E',H,I] u16
+//            with E' = E + shared.  shared = 1: the always-on shared expert is
+//            folded in as expert E (tau_launch_moe_routing_shared_ex writes the
+//            routes from the [T, E+1] logits, then tau_launch_moe_prefill_ex runs
+//            from those routes with E+1 experts and K+1 picks)
 //   out.bin: int32 status, capacity; routes [T,2K] f32; meta [2E+2], offsets [E+1],
 //            slots [cap], tiles [cap/tile_rows] int32; activated [cap,I],
 //            contributions [T*K,H], output [T,H] u16
@@ -59,9 +63,11 @@ int main(int argc, char** argv) {
     }
     FILE* f = std::fopen(argv[1], "rb");
     if (!f) return 2;
-    int h[8];
-    if (std::fread(h, sizeof(int), 8, f) != 8) return 2;
-    const int T = h[0], H = h[1], I = h[2], E = h[3], K = h[4], M = h[5], layout = h[6], ldt = h[7];
+    int h[9];
+    if (std::fread(h, sizeof(int), 9, f) != 9) return 2;
+    const int T = h[0], H = h[1], I = h[2], E0 = h[3], K0 = h[4], M = h[5], layout = h[6], ldt = h[7];
+    const int shared = h[8];
+    const int E = E0 + shared, K = K0 + shared;  // the schedule's experts and picks
     Buf<uint16_t> x((size_t)T * H, 0), gu((size_t)E * 2 * I * H, 0), dn((size_t)E * H * I, 0);
     Buf<unsigned char> logits((size_t)T * E * ((ldt & 1) ? 2 : 4), 0);
     if (!read(f, x) || !read(f, logits) || !read(f, gu) || !read(f, dn)) return 2;
@@ -72,10 +78,13 @@ int main(int argc, char** argv) {
     Buf<float> routes(sz[0] / 4, -7.f);
     Buf<int> meta(sz[1] / 4, -7), offsets(sz[2] / 4, -7), slots(sz[3] / 4, -7), tiles(sz[4] / 4, -7);
     Buf<uint16_t> act(sz[5] / 2, 0x7777), con(sz[6] / 2, 0x7777), out((size_t)T * H, 0x7777);
-    const int status = tau_launch_moe_prefill_ex(x.data(), logits.data(), ldt, gu.data(), dn.data(), routes.data(),
-                                                 meta.data(), offsets.data(), slots.data(), tiles.data(), act.data(),
-                                                 con.data(), out.data(), T, H, I, E, K, M, cap, layout, nullptr,
-                                                 nullptr, nullptr);
+    int status = 0;
+    if (shared) status = tau_launch_moe_routing_shared_ex(logits.data(), ldt, routes.data(), T, E0, K0, nullptr);
+    if (status == 0)
+        status = tau_launch_moe_prefill_ex(x.data(), shared ? nullptr : logits.data(), ldt, gu.data(), dn.data(),
+                                           routes.data(), meta.data(), offsets.data(), slots.data(), tiles.data(),
+                                           act.data(), con.data(), out.data(), T, H, I, E, K, M, cap, layout,
+                                           nullptr, nullptr, nullptr);
     FILE* o = std::fopen(argv[2], "wb");
     if (!o) return 2;
     std::fwrite(&status, 4, 1, o);
