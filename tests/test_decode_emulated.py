@@ -55,14 +55,19 @@ def run(bins, which, x, logits, gu, dn, layout, bf16_logits=True, raw=False):
     I = two_i // 2
     K = run.K
     ldt = (1 if bf16_logits else 0) | (0x100 if raw else 0)
-    from frag16_host import frag16_permute
-    gu_b, dn_b = bf16_bits(gu), bf16_bits(dn)
-    if layout == 1:
-        gu_b, dn_b = frag16_permute(gu_b), frag16_permute(dn_b)
-    lg = bf16_bits(logits) if bf16_logits else np.ascontiguousarray(logits, np.float32)
-    hdr = np.array([T, H, I, E, K, layout, ldt], np.int32)
-    src, dst = work / f"in_{which}.bin", work / f"out_{which}.bin"
-    src.write_bytes(hdr.tobytes() + bf16_bits(x).tobytes() + lg.tobytes() + gu_b.tobytes() + dn_b.tobytes())
+    key = (id(x), id(logits), id(gu), id(dn), layout, ldt, K)
+    src, dst = work / "in.bin", work / f"out_{which}.bin"
+    if run.encoded != key:  # both builds read the same encoded input
+        from frag16_host import frag16_permute
+        gu_b, dn_b = bf16_bits(gu), bf16_bits(dn)
+        if layout == 1:
+            gu_b, dn_b = frag16_permute(gu_b), frag16_permute(dn_b)
+        lg = bf16_bits(logits) if bf16_logits else np.ascontiguousarray(logits, np.float32)
+        hdr = np.array([T, H, I, E, K, layout, ldt], np.int32)
+        with open(src, "wb") as f:
+            for part in (hdr, bf16_bits(x), lg, gu_b, dn_b):
+                f.write(memoryview(np.ascontiguousarray(part)).cast("B"))
+        run.encoded = key
     subprocess.run([str(exe[which]), str(src), str(dst)], check=True, timeout=900)
     raw_out = np.fromfile(dst, np.uint8)
     o = 0
@@ -81,12 +86,29 @@ def run(bins, which, x, logits, gu, dn, layout, bf16_logits=True, raw=False):
             "output": take(np.uint16, T * H).reshape(T, H), "cap": int(cap)}
 
 
+def banks(rng, shape):
+    """BF16-exact expert weights ~N(0, 0.05^2).  Full-size banks (about a
+    gigabyte) take each expert's matrix as a different shifted window of one
+    random pool, so every expert still holds different values at every
+    position while generation stays a few seconds."""
+    E, n = shape[0], shape[1] * shape[2]
+    if E * n <= 1 << 24:
+        return from_bits(bf16_bits(rng.standard_normal(shape) * 0.05))
+    step = 4099
+    pool = from_bits(bf16_bits(rng.standard_normal(n + E * step).astype(np.float32) * 0.05))
+    out = np.empty((E, n), np.float32)
+    for e in range(E):
+        out[e] = pool[e * step:e * step + n]
+    return out.reshape(shape)
+
+
 CASES = [  # T, H, I, E, K, layout, bf16 logits, raw weights, NaN row
     (16, 256, 256, 8, 2, 1, True, False, False),
     (5, 256, 512, 16, 4, 0, False, False, False),
     (12, 256, 256, 24, 3, 1, True, True, False),
     (8, 256, 256, 8, 2, 1, True, False, True),
     (64, 256, 256, 32, 8, 1, True, False, False),  # skewed below: experts with 17-64 rows (row groups 2-4)
+    (64, 2048, 768, 128, 8, 1, True, False, False),  # the c2 (Qwen3-30B-A3B decode) layer at full size
 ]
 
 
@@ -95,18 +117,19 @@ def test_decode_path_emulated(bins, oracle, case):
     T, H, I, E, K, layout, bf16_logits, raw, nan_row = CASES[case]
     rng = np.random.default_rng(40 + case)
     x = from_bits(bf16_bits(rng.standard_normal((T, H))))
-    gu = from_bits(bf16_bits(rng.standard_normal((E, 2 * I, H)) * 0.05))
-    dn = from_bits(bf16_bits(rng.standard_normal((E, H, I)) * 0.05))
+    gu = banks(rng, (E, 2 * I, H))
+    dn = banks(rng, (E, H, I))
     logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
     if bf16_logits:
         logits = from_bits(bf16_bits(logits))
     if nan_row:
         logits[3, 1] = np.nan
-    if T == 64:  # a per-expert popularity bias: some experts take most tokens
+    if T == 64 and E == 32:  # a per-expert popularity bias: some experts take most tokens
         logits = logits + (rng.standard_normal(E) * 1.5).astype(np.float32)
         if bf16_logits:
             logits = from_bits(bf16_bits(logits))
     run.K = K
+    run.encoded = None
     two = run(bins, "two", x, logits, gu, dn, layout, bf16_logits, raw)
     one = run(bins, "one", x, logits, gu, dn, layout, bf16_logits, raw)
     for key in ("routes", "meta", "offsets", "slots", "tiles", "contributions", "output"):
@@ -121,7 +144,7 @@ def test_decode_path_emulated(bins, oracle, case):
     if nan_row:
         assert two["meta"][2 * E] == 1 and np.all(np.isnan(from_bits(two["output"])))
         return
-    if T == 64:
+    if T == 64 and E == 32:
         assert two["meta"][:E].max() > 32  # several 16-row groups for one expert
     ids, w = oracle.route(logits, K, normalize=not raw)
     np.testing.assert_array_equal(two["routes"][:, :K].astype(np.int64), ids)
