@@ -109,6 +109,7 @@ CASES = [  # T, H, I, E, K, layout, bf16 logits, raw weights, NaN row
     (8, 256, 256, 8, 2, 1, True, False, True),
     (64, 256, 256, 32, 8, 1, True, False, False),  # skewed below: experts with 17-64 rows (row groups 2-4)
     (64, 2048, 768, 128, 8, 1, True, False, False),  # the c2 (Qwen3-30B-A3B decode) layer at full size
+    (16, 256, 512, 8, 2, 1, False, False, False),  # the c1 tiny layer's shape, f32 router logits
 ]
 
 
