@@ -467,9 +467,12 @@ int launch_decode_layer(const void* input, const void* logits, int logits_dtype,
                         int top_k, int capacity, int weight_layout, int* receipts, hipStream_t s) {
     if (!logits || tokens > kLayerMaxTokens || experts > 256 || top_k > 32) return kNotApplicable;
     // Splits per expert: about one workgroup per CU, each split's down
-    // columns a whole number of 64-column groups.
+    // columns a whole number of 64-column groups.  Every split recomputes its
+    // expert's whole gate_up (from L2 after the first), so splits stop at 4
+    // (with fewer than 64 experts the grid then leaves CUs idle; the benchmark
+    // layers have 128).
     int splits = 1;
-    while (experts * splits * 2 <= 256 && hidden % (64 * splits * 2) == 0) splits *= 2;
+    while (splits < 4 && experts * splits * 2 <= 256 && hidden % (64 * splits * 2) == 0) splits *= 2;
     const size_t lds = layer_act_offset(tokens, top_k) + (size_t)tokens * intermediate * 2;
     // Whole K batches for both projections (256 = the widest batch, 8 x 32).
     if (lds > 150 * 1024 || hidden % 256 || intermediate % 256) return kNotApplicable;
