@@ -37,10 +37,23 @@ def kernel_resources(tmp_path, defines):
     return out
 
 
-@pytest.mark.parametrize("defines", [[], ["-DTAU_M256_BIG_WAVES"], ["-DTAU_SPLIT_ROWS=64"]],
-                         ids=["default", "big_waves", "split64"])
-def test_mfma_tiles_compile_without_spills(tmp_path, defines):
-    res = kernel_resources(tmp_path, defines)
+BUILDS = {"default": [], "big_waves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"]}
+
+
+@pytest.fixture(scope="module")
+def resources(tmp_path_factory):
+    """Kernel resources of every build, compiled side by side."""
+    import concurrent.futures
+    dirs = {k: tmp_path_factory.mktemp(k) for k in BUILDS}
+    with concurrent.futures.ThreadPoolExecutor(len(BUILDS)) as ex:
+        futs = {k: ex.submit(kernel_resources, dirs[k], d) for k, d in BUILDS.items()}
+        return {k: f.result() for k, f in futs.items()}
+
+
+@pytest.mark.parametrize("build", list(BUILDS))
+def test_mfma_tiles_compile_without_spills(resources, build):
+    defines = BUILDS[build]
+    res = resources[build]
     mfma = {k: v for k, v in res.items() if "mfma_gemm" in k}
     assert len(mfma) >= 20, sorted(res)
     for name, r in mfma.items():

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def test_expf_glibc_matches_system_expf_on_every_float(tmp_path):
     exe = tmp_path / "libm_expf_check"
-    subprocess.run(["g++", "-std=c++17", "-O2", "-o", str(exe),
+    subprocess.run(["g++", "-std=c++17", "-O2", "-fopenmp", "-o", str(exe),
                     os.path.join(ROOT, "tests", "libm_expf_check.cpp"), "-lm"], check=True)
     r = subprocess.run([str(exe), "1"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
