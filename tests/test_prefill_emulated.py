@@ -201,3 +201,48 @@ def test_folded_shared_expert_c4_dims(bins, oracle):
     routed = oracle.moe(x, ids, w, gu[:E], dn[:E])
     ref = oracle.shared_combine_f32(x, w_s, oracle.dense_mlp(x, gu[E], dn[E]), routed)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-2
+
+
+@pytest.mark.parametrize("T,E,K,shared,bias", [(4096, 128, 8, 0, "normal"), (2048, 512, 10, 1, "zipf"),
+                                               (8192, 128, 8, 0, "none")], ids=["c3", "c4", "c5p"])
+def test_full_size_routing_and_dispatch(bins, oracle, tau, T, E, K, shared, bias):
+    """Routing and the multi-workgroup dispatch (32 chunks of whole 64-token
+    passes) at the benchmark layers' token, expert and top-k counts, with the
+    row block the library selects for the real hidden/intermediate sizes:
+    c3's per-expert N(0,1) router bias, c4's Zipf(1.1) popularity bias with the
+    shared expert folded in as expert 512, c5 prefill's uniform routing.
+    Hidden and intermediate are 64 so the projections stay cheap; routes,
+    meta, offsets, slots and tiles must equal the oracle's bit for bit (the
+    reference's stable token-ascending order, routing.rs:159-227), and the
+    output is checked against the oracle's BF16 contract."""
+    dims = {"c3": (2048, 768), "c4": (2048, 512), "c5p": (4096, 1536)}
+    H, I = 64, 64
+    rng = np.random.default_rng(T + E)
+    x = from_bits(bf16_bits(rng.standard_normal((T, H))))
+    gu = from_bits(bf16_bits(rng.standard_normal((E + shared, 2 * I, H)) * 0.05))
+    dn = from_bits(bf16_bits(rng.standard_normal((E + shared, H, I)) * 0.05))
+    logits = rng.standard_normal((T, E + shared)).astype(np.float32)
+    if bias == "normal":
+        logits[:, :E] += rng.standard_normal(E).astype(np.float32)
+    elif bias == "zipf":
+        logits[:, :E] += np.log(1.0 / np.arange(1, E + 1) ** 1.1)[rng.permutation(E)].astype(np.float32)
+    logits = from_bits(bf16_bits(logits))
+    real_h, real_i = dims["c3" if T == 4096 else "c4" if shared else "c5p"]
+    M = tau.ffi.select_tile_rows(T, E + shared, K + shared, real_h, real_i)
+    res = run(bins, "base", x, logits, gu, dn, K, M, 0, shared=shared)
+    ids, w = oracle.route(logits[:, :E], K)
+    r = res["routes"]
+    np.testing.assert_array_equal(r[:, :K].astype(np.int64), ids)
+    np.testing.assert_array_equal(r[:, K + shared:2 * K + shared], w)
+    if shared:
+        gate = oracle.sigmoid(logits[:, E])
+        assert np.all(r[:, K] == E)
+        np.testing.assert_array_equal(r[:, 2 * K + 1], gate)
+        ids = np.concatenate([ids, np.full((T, 1), E, np.int64)], 1)
+        w = np.concatenate([w, gate[:, None]], 1).astype(np.float32)
+    meta, offsets, slots, tiles = oracle.dispatch(ids, E + shared, M, res["cap"])
+    for key, ref in (("meta", meta), ("offsets", offsets), ("slots", slots), ("tiles", tiles)):
+        np.testing.assert_array_equal(res[key], ref, err_msg=key)
+    ref = oracle.moe(x, ids, w, gu, dn, bf16=True)
+    got = from_bits(res["output"])
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3
