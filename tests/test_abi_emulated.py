@@ -314,3 +314,17 @@ def test_shared_expert_path(exe, oracle, tokens, layout):
     ref32 = oracle.shared_combine_f32(x, gate_w, oracle.dense_mlp(x, gu, dn), routed)
     assert rel_l2(got, ref16) <= 2e-3
     assert rel_l2(got, ref32) <= 1e-2
+
+
+@pytest.mark.parametrize("shape", [(3, 48, 128), (64, 192), (2, 1536, 2048)])
+def test_pack_weights_matches_header_order(exe, shape):
+    """tau_moe_pack_weights writes the FRAG16 order the header defines (its
+    piece formula restated by frag16_host.frag16_permute, itself pinned to the
+    literal loop in test_host)."""
+    from frag16_host import frag16_permute
+    rng = np.random.default_rng(len(shape))
+    src = rng.integers(0, 1 << 16, size=shape, dtype=np.uint16)
+    e, r, c = (1, *shape) if len(shape) == 2 else shape
+    st, out = call(exe, 10, [e, r, c], [src, np.zeros_like(src)])
+    assert st == 0
+    np.testing.assert_array_equal(out[1], frag16_permute(src))

@@ -25,6 +25,7 @@
 //       gate_weight, routed, activated_ws, shared_ws, output, residual,
 //       [tokens, hidden, shared_intermediate, weight_layout]); output = routed
 //       when b7 is empty (the in-place form)
+//  10 tau_moe_pack_weights(b0 src, b1 dst, [experts, rows, columns])
 // Buffers live in an arena mapped at 0x7e0080000000 (low address words with
 // bit 31 set).
 #include <sys/mman.h>
@@ -124,6 +125,9 @@ int main(int argc, char** argv) {
         case 9:
             status = tau_launch_moe_shared_expert_ex(b[0], b[1], b[2], b[3], b[4], b[5], b[6], b[7] ? b[7] : b[4],
                                                      I(0), I(1), I(2), I(3), b[8], nullptr);
+            break;
+        case 10:
+            status = tau_moe_pack_weights(b[0], b[1], I(0), I(1), I(2), nullptr);
             break;
         default:
             return 2;
