@@ -104,26 +104,31 @@ def banks(rng, shape):
     return out.reshape(shape)
 
 
-CASES = [  # T, H, I, E, K, layout, bf16 logits, raw weights, NaN row
-    (16, 256, 256, 8, 2, 1, True, False, False),
-    (5, 256, 512, 16, 4, 0, False, False, False),
-    (12, 256, 256, 24, 3, 1, True, True, False),
-    (8, 256, 256, 8, 2, 1, True, False, True),
-    (64, 256, 256, 32, 8, 1, True, False, False),  # skewed below: experts with 17-64 rows (row groups 2-4)
-    (64, 2048, 768, 128, 8, 1, True, False, False),  # the c2 (Qwen3-30B-A3B decode) layer at full size
-    (16, 256, 512, 8, 2, 1, False, False, False),  # the c1 tiny layer's shape, f32 router logits
-    (32, 4096, 1536, 16, 8, 1, True, False, False),  # c5 decode's sizes (H 4096, I 1536, 32 tokens), 16 experts
+CASES = [  # T, H, I, E, K, layout, bf16 logits, raw weights, NaN row, tied logits
+    (16, 256, 256, 8, 2, 1, True, False, False, False),
+    (5, 256, 512, 16, 4, 0, False, False, False, False),
+    (12, 256, 256, 24, 3, 1, True, True, False, False),
+    (8, 256, 256, 8, 2, 1, True, False, True, False),
+    (64, 256, 256, 32, 8, 1, True, False, False, False),  # skewed below: experts with 17-64 rows (row groups 2-4)
+    (64, 2048, 768, 128, 8, 1, True, False, False, False),  # the c2 (Qwen3-30B-A3B decode) layer at full size
+    (16, 256, 512, 8, 2, 1, False, False, False, False),  # the c1 tiny layer's shape, f32 router logits
+    (32, 4096, 1536, 16, 8, 1, True, False, False, False),  # c5 decode's sizes (H 4096, I 1536, 32 tokens), 16 experts
+    (24, 256, 128, 60, 20, 0, True, False, False, True),  # E not a multiple of 8, K > 16, heavy ties
+    (40, 256, 128, 128, 8, 1, False, False, False, True),  # f32 logits on a coarse grid
+    (64, 256, 64, 250, 3, 1, True, False, False, False),
 ]
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_decode_path_emulated(bins, oracle, case):
-    T, H, I, E, K, layout, bf16_logits, raw, nan_row = CASES[case]
+    T, H, I, E, K, layout, bf16_logits, raw, nan_row, ties = CASES[case]
     rng = np.random.default_rng(40 + case)
     x = from_bits(bf16_bits(rng.standard_normal((T, H))))
     gu = banks(rng, (E, 2 * I, H))
     dn = banks(rng, (E, H, I))
     logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    if ties:  # a coarse grid: many equal logits per row, broken by expert id
+        logits = np.round(logits * 4) / 4
     if bf16_logits:
         logits = from_bits(bf16_bits(logits))
     if nan_row:
