@@ -16,30 +16,55 @@ def available() -> bool:
     return os.path.exists(CXX) or shutil.which(CXX) is not None
 
 
-def build(out_dir, driver: str, variants):
-    """variants: {name: (sources, defines)}; returns {name: binary path}."""
-    out_dir = str(out_dir)
-    src = os.path.join(out_dir, "src")
-    if not os.path.isdir(src):
+_shared = {}  # per process: the rewritten sources and every library object built so far
+
+
+def _library_tree():
+    """The library sources rewritten for the emulator, once per process."""
+    if "src" not in _shared:
+        import atexit
+        import tempfile
+        top = tempfile.mkdtemp(prefix="tau_emu_")
+        atexit.register(shutil.rmtree, top, True)
+        src = os.path.join(top, "src")
         sys.path.insert(0, os.path.join(ROOT, "tests", "wave_emu"))
         import prep
         prep.main(ROOT, src)
+        _shared["src"] = src
+        _shared["objects"] = {}
+    return _shared["src"]
+
+
+def build(out_dir, driver: str, variants):
+    """variants: {name: (sources, defines)}; returns {name: binary path}.
+    Library objects are compiled once per process and shared by every driver."""
+    out_dir = str(out_dir)
+    src = _library_tree()
+    objects = _shared["objects"]
     csrc = os.path.join(src, "a", "csrc")
     inc = ["-I", os.path.join(ROOT, "tests", "wave_emu"), "-I", csrc]
     flags = ["-std=c++20", "-O1", "-w"]
-    jobs = {}  # (file, defines) -> object
+    jobs = {}  # (file, defines) -> object still to compile
+    drv = os.path.join(ROOT, "tests", "wave_emu", driver)
     for sources, defines in variants.values():
-        for f in [os.path.join(ROOT, "tests", "wave_emu", driver)] + [os.path.join(csrc, s) for s in sources]:
+        for f in [drv] + [os.path.join(csrc, s) for s in sources]:
             key = (f, tuple(defines))
+            if key in objects:
+                continue
             tag = os.path.splitext(os.path.basename(f))[0] + "".join(d.replace("-D", "_") for d in defines)
-            jobs[key] = os.path.join(out_dir, tag + ".o")
+            jobs[key] = os.path.join(out_dir if f == drv else os.path.dirname(src), tag + ".o")
 
     def compile_one(item):
         (f, defines), obj = item
         subprocess.run([CXX, *flags, *defines, *inc, "-c", f, "-o", obj], check=True)
 
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-        list(ex.map(compile_one, jobs.items()))
+    if jobs:
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+            list(ex.map(compile_one, jobs.items()))
+    for key, obj in jobs.items():
+        if key[0] != drv:
+            objects[key] = obj
+    jobs.update({k: v for k, v in objects.items()})
     out = {}
     for name, (sources, defines) in variants.items():
         objs = [jobs[(os.path.join(ROOT, "tests", "wave_emu", driver), tuple(defines))]] + \
