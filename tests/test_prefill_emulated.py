@@ -12,9 +12,9 @@ routing gives both full and nearly empty 256-row blocks.  Checks:
     for bit, the output is within the BF16 contract's tolerance of the oracle
     (the emulator's MFMA sums K in order; the hardware's order is not claimed);
   * -DTAU_M256_BIG_WAVES (2x2 waves of 128x128: 32-bit copy offsets from a
-    scalar base, the variant whose one GPU run faulted) and
+    scalar base, the variant whose one GPU run faulted),
     -DTAU_SPLIT_ROWS=64 / 128 (lightly filled blocks on the shorter tile in a
-    second launch) reproduce the shipped build's activated rows, contributions
+    second launch) and the first two together reproduce the shipped build's activated rows, contributions
     and output bit for bit: per output element they issue the same MFMA
     sequence, so any difference is an addressing or scheduling bug."""
 import os
@@ -32,7 +32,8 @@ torch = pytest.importorskip("torch")
 SOURCES = ["combine.cpp", "decode.cpp", "decode_layer.cpp", "decode_moe.cpp", "elementwise.cpp",
            "grouped_gemm.cpp", "moe.cpp", "norm.cpp", "router.cpp", "routing.cpp"]
 VARIANTS = {"base": [], "bigwaves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"],
-            "split128": ["-DTAU_SPLIT_ROWS=128"]}
+            "split128": ["-DTAU_SPLIT_ROWS=128"],
+            "bigwaves_split64": ["-DTAU_M256_BIG_WAVES", "-DTAU_SPLIT_ROWS=64"]}
 
 
 @pytest.fixture(scope="module")
@@ -125,7 +126,7 @@ def test_256_row_tiles_and_variants(bins, oracle, layout):
     meta = check_against_oracle(oracle, base, x, logits, gu, dn, K, 256)
     counts = meta[:E]
     assert counts.max() > 128 and (counts[counts > 0] <= 64).any()  # both kinds of block
-    for v in ("bigwaves", "split64", "split128"):
+    for v in ("bigwaves", "split64", "split128", "bigwaves_split64"):
         res = run(bins, v, x, logits, gu, dn, K, 256, layout)
         for key in ("routes", "meta", "slots", "tiles", "contributions", "output"):
             np.testing.assert_array_equal(res[key].view(np.uint32) if res[key].dtype == np.float32 else res[key],
