@@ -387,6 +387,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm(GemmArgs p) {
     }
 }
 
+// -DTAU_SPLIT_ROWS=32|64|128: 256-row dispatch blocks with at most that many
+// live rows run in a second launch on the weight-streaming kernel (two 16-row
+// groups), the 64x256 or the 128x128 MFMA tile (default off).
+#ifdef TAU_SPLIT_ROWS
+constexpr int kSplitRows = TAU_SPLIT_ROWS;
+static_assert(kSplitRows == 32 || kSplitRows == 64 || kSplitRows == 128, "TAU_SPLIT_ROWS is 32, 64 or 128");
+#else
+constexpr int kSplitRows = 0;
+#endif
+
 // Pipelined weight-streaming kernel for 16-byte-aligned operands.  Each wave
 // owns NB 16-column blocks (gate and up blocks for SiLU) of one 16-row block;
 // loads carry no branches (invalid rows are clamped to a valid address and
@@ -410,7 +420,11 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
         p.receipt[3] = W; p.receipt[4] = 2;
     }
     const int n_groups = (p.n + 16 * NB - 1) / (16 * NB);
-    const int live = live_blocks(p, R);
+    // Small-block split (32 rows): the dispatch blocks are block_stride rows
+    // apart and this kernel takes the blocks with at most R live rows.
+    constexpr bool kStrided = kSplitRows == R;
+    const int stride = kStrided && p.block_stride ? p.block_stride : R;
+    const int live = live_blocks(p, stride);
     const int total = live * n_groups;
     const int groups = (total + W - 1) / W;
     const int per_xcd = (groups + kXcds - 1) / kXcds;
@@ -418,23 +432,39 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
     const int item = group * W + wave;
     if (group < 0 || group >= groups || item >= total) return;
     const int m_tile = item / n_groups, ng = item - m_tile * n_groups;
+    const int row0 = m_tile * stride;
+    if (kStrided && p.split_rows > 0) {
+        // Padding is a suffix of an expert's block: the block has more than R
+        // live rows iff row row0 + R holds an assignment (the MFMA tile's).
+        const int probe = row0 + R;
+        if (probe < p.rows && probe < row0 + stride && p.slots[probe] >= 0 && p.slots[probe] < p.assignments)
+            return;
+    }
     const int expert = p.tiles ? p.tiles[m_tile] : 0;
     if (expert < 0) {
         if constexpr (EPI == kEpiStoreBf16) {
             uint16_t* out = (uint16_t*)p.out;
-            for (int i = lane; i < R * 16 * NB; i += 64) {
-                const int r = m_tile * R + i / (16 * NB), c = ng * 16 * NB + i % (16 * NB);
+            for (int i = lane; i < stride * 16 * NB; i += 64) {
+                const int r = row0 + i / (16 * NB), c = ng * 16 * NB + i % (16 * NB);
                 if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
             }
         }
         return;
+    }
+    if constexpr (kStrided && EPI != kEpiScatterWeighted) {
+        // The block's rows past R are padding: zeros, as in the MFMA tile.
+        uint16_t* out = (uint16_t*)p.out;
+        for (int i = lane; i < (stride - R) * 16 * NB; i += 64) {
+            const int r = row0 + R + i / (16 * NB), c = ng * 16 * NB + i % (16 * NB);
+            if (r < p.rows && c < p.n) out[(size_t)r * p.ldo + c] = 0;
+        }
     }
     const int kofs = (lane >> 4) * 8;
     bool x_ok[RT];
     const uint16_t* xs[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int row = m_tile * R + rt * 16 + (lane & 15);
+        const int row = row0 + rt * 16 + (lane & 15);
         bool ok = row < p.rows;
         long x_row = ok ? row : 0;
         if constexpr (AM == kAGather) {
@@ -539,7 +569,7 @@ __global__ __launch_bounds__(64 * W) void stream_gemm_fast(GemmArgs p) {
     // token row l%16 of its group.
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int orow = m_tile * R + rt * 16 + (lane & 15);
+        const int orow = row0 + rt * 16 + (lane & 15);
         if (orow >= p.rows) continue;
         long out_row = orow;
         float wt = 1.0f;
@@ -640,14 +670,6 @@ __device__ __forceinline__ void lds_dma16_off(const uint16_t* base, uint32_t off
 // MFMAs (lgkmcnt) before the barrier that lets a stage be overwritten.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// -DTAU_SPLIT_ROWS=64|128: 256-row dispatch blocks with at most that many live
-// rows run on the 64x256 (or 128x128) tile in a second launch (default off).
-#ifdef TAU_SPLIT_ROWS
-constexpr int kSplitRows = TAU_SPLIT_ROWS;
-static_assert(kSplitRows == 64 || kSplitRows == 128, "TAU_SPLIT_ROWS is 64 or 128");
-#else
-constexpr int kSplitRows = 0;
-#endif
 
 // IG >= 0 asks the compiler's instruction-group scheduler for strategy IG
 // (__builtin_amdgcn_iglp_opt) in the K loop; 1 interleaves the fragment reads
@@ -999,7 +1021,7 @@ int launch_stream(const GemmArgs& p, bool aligned, hipStream_t s) {
     // K steps per batch.
     constexpr int NB = WL == kWeightsFrag16 ? 2 : (EPI == kEpiSilu ? 1 : 4);
     constexpr int U = WL == kWeightsFrag16 ? 8 : 4;
-    const int rows = 16 * RT;
+    const int rows = p.block_stride ? p.block_stride : 16 * RT;  // rows between the row blocks
     const long m_blocks = (p.rows + rows - 1) / rows;
     if (!aligned) {
         if (RT != 1 || WL != kWeightsRowMajor) return kInvalid;
@@ -1045,13 +1067,17 @@ int launch_by_rows(const GemmArgs& p, int bm, bool aligned, hipStream_t s) {
                         // Blocks with at most kSplitRows live rows (an expert's
                         // tail or a lightly routed expert) run on the shorter
                         // tile, the rest on the 256-row tile.
+                        // The receipt keeps describing the 256-row tile.
                         GemmArgs big = p, small = p;
                         big.split_rows = small.split_rows = kSplitRows;
                         small.block_stride = 256;
+                        small.receipt = nullptr;
                         const int code =
                             launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(big, s);
                         if (code) return code;
-                        if constexpr (kSplitRows == 64) return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(small, s);
+                        if constexpr (kSplitRows == 32) return launch_stream<AM, EPI, 2, WL>(small, aligned, s);
+                        else if constexpr (kSplitRows == 64)
+                            return launch_mfma<64, 256, 1, 4, 2, AM, EPI, 64, WL>(small, s);
                         else return launch_mfma<128, 128, 2, 2, 2, AM, EPI, 64, WL, 1>(small, s);
                     }
                     return launch_mfma<256, 256, kM256WavesM, kM256WavesN, 2, AM, EPI, 64, WL, 1>(p, s);
