@@ -252,3 +252,9 @@ def test_full_size_routing_and_dispatch(bins, oracle, tau, T, E, K, shared, bias
     ref = oracle.moe(x, ids, w, gu, dn, bf16=True)
     got = from_bits(res["output"])
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3
+    if shared:  # Zipf routing: most blocks hold a few rows, the 32-row split's case
+        counts = meta[:E]
+        assert ((counts > 0) & (counts <= 32)).sum() > (counts > 0).sum() // 2
+        split = run(bins, "split32", x, logits, gu, dn, K, M, 0, shared=shared)
+        for key in ("routes", "slots", "contributions", "output"):
+            np.testing.assert_array_equal(split[key], res[key], err_msg=key)
