@@ -26,6 +26,8 @@
 #include "kernels.hpp"
 #include "mfma_copy_plan.hpp"
 
+#include <type_traits>
+
 namespace tau_amd {
 
 namespace {
@@ -395,6 +397,15 @@ constexpr int kSplitRows = TAU_SPLIT_ROWS;
 static_assert(kSplitRows == 32 || kSplitRows == 64 || kSplitRows == 128, "TAU_SPLIT_ROWS is 32, 64 or 128");
 #else
 constexpr int kSplitRows = 0;
+#endif
+
+// With -DTAU_M256_BIG_WAVES the 128x128 wave tiles skip the MFMAs of their
+// 32-row fragments that hold only padding (-DTAU_BIG_WAVE_NO_SKIP keeps
+// every MFMA, for comparison).
+#ifdef TAU_BIG_WAVE_NO_SKIP
+constexpr bool kBigWaveSkip = false;
+#else
+constexpr bool kBigWaveSkip = true;
 #endif
 
 // Pipelined weight-streaming kernel for 16-byte-aligned operands.  Each wave
@@ -879,29 +890,82 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             }
         }
     };
-    for (int kt = 0; kt < nk; ++kt) {
-        // Tile kt's loads are done once at most the later-issued loads remain
-        // (VMEM loads complete in order).
-        if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
-        else wait_vmcnt<0>();
-        lds_barrier();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
-        const uint16_t* Bs = As + BM * BK;
-        if constexpr (!kBigWave) {
-            if (!wave_rows_live) continue;
+    if constexpr (kBigWave && kBigWaveSkip && (AM == kAGather || EPI == kEpiScatterWeighted)) {
+        // 128-row wave tiles: padding is a suffix of the block, so the 32-row
+        // fragments holding live rows are a prefix of the wave's MI.  The K
+        // loop runs with the MFMAs and A fragment reads of that prefix only;
+        // the other fragments keep zero accumulators (their rows are written
+        // as zeros or dropped).  The count is wave-uniform and chosen once,
+        // outside the K loop, so the accumulators never move.
+        static_assert(MI == 4, "128-row wave tiles hold four 32-row fragments");
+        int nl = 0;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) nl += row_src[wm * TM + i * 32] >= 0;
+        nl = __builtin_amdgcn_readfirstlane(nl);
+        auto k_loop = [&](auto nl_tag) {
+            constexpr int NL = decltype(nl_tag)::value;
+            for (int kt = 0; kt < nk; ++kt) {
+                if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
+                else wait_vmcnt<0>();
+                lds_barrier();
+                if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+                if constexpr (NL > 0) {
+                    const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
+                    const uint16_t* Bs = As + BM * BK;
+                    if constexpr (IG >= 0) __builtin_amdgcn_iglp_opt(IG);
+                    bf16x8 af[2][MI], bfr[2][NI];
+                    auto frags_nl = [&](int ks, bf16x8* a_, bf16x8* b_) {
+                        bf16x8 a_all[MI];
+                        frags(As, Bs, ks, a_all, b_);  // reads of fragments past NL are dead code
+#pragma unroll
+                        for (int i = 0; i < NL; ++i) a_[i] = a_all[i];
+                    };
+                    frags_nl(0, af[0], bfr[0]);
+#pragma unroll
+                    for (int ks = 0; ks < BK / 16; ++ks) {
+                        if (ks + 1 < BK / 16) frags_nl(ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+#pragma unroll
+                        for (int i = 0; i < NL; ++i)
+#pragma unroll
+                            for (int j = 0; j < NI; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j],
+                                                                                    acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        };
+        switch (nl) {
+            case 4: k_loop(std::integral_constant<int, 4>{}); break;
+            case 3: k_loop(std::integral_constant<int, 3>{}); break;
+            case 2: k_loop(std::integral_constant<int, 2>{}); break;
+            case 1: k_loop(std::integral_constant<int, 1>{}); break;
+            default: k_loop(std::integral_constant<int, 0>{}); break;
         }
-        if constexpr (IG >= 0) __builtin_amdgcn_iglp_opt(IG);
-        bf16x8 af[2][MI], bfr[2][NI];
-        frags(As, Bs, 0, af[0], bfr[0]);
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            if (ks + 1 < BK / 16) frags(As, Bs, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NI; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+    } else {
+        for (int kt = 0; kt < nk; ++kt) {
+            // Tile kt's loads are done once at most the later-issued loads remain
+            // (VMEM loads complete in order).
+            if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * L>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+            const uint16_t* As = smem + (kt % STAGES) * STAGE_ELEMS;
+            const uint16_t* Bs = As + BM * BK;
+            if constexpr (!kBigWave) {
+                if (!wave_rows_live) continue;
+            }
+            if constexpr (IG >= 0) __builtin_amdgcn_iglp_opt(IG);
+            bf16x8 af[2][MI], bfr[2][NI];
+            frags(As, Bs, 0, af[0], bfr[0]);
+    #pragma unroll
+            for (int ks = 0; ks < BK / 16; ++ks) {
+                if (ks + 1 < BK / 16) frags(As, Bs, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+    #pragma unroll
+                for (int i = 0; i < MI; ++i)
+    #pragma unroll
+                    for (int j = 0; j < NI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+            }
         }
     }
     __syncthreads();  // stages are reused for the output tile

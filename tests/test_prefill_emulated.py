@@ -153,7 +153,7 @@ def test_shorter_tiles(bins, oracle, M, layout, bf16_logits):
     check_against_oracle(oracle, res, x, logits, gu, dn, K, M, bf16_logits)
 
 
-@pytest.mark.parametrize("H,I,T", [(2048, 768, 320), (4096, 1536, 272)], ids=["c3_dims", "c5p_dims"])
+@pytest.mark.parametrize("H,I,T", [(2048, 768, 346), (4096, 1536, 272)], ids=["c3_dims", "c5p_dims"])
 def test_benchmark_layer_dims(bins, oracle, H, I, T):
     """The 256-row MFMA tile at the hidden and intermediate sizes of the
     30B-A3B (c3) and 235B-A22B (c5 prefill) layers: full-length K loops
@@ -168,7 +168,9 @@ def test_benchmark_layer_dims(bins, oracle, H, I, T):
         futs = {v: ex.submit(run, bins, v, x, logits, gu, dn, K, 256, 1) for v in ("base", "bigwaves")}
         res = {v: f.result() for v, f in futs.items()}
     meta = check_against_oracle(oracle, res["base"], x, logits, gu, dn, K, 256)
-    assert meta[0] > 256 and meta[0] % 256 <= 64  # a full block and a nearly empty one
+    assert meta[0] > 256 and meta[0] % 256 <= 96  # a full block and a partly empty one
+    # 128-row wave tiles see 0 to 4 live 32-row fragments across the blocks
+    # (c3 sizes: about 90 rows in expert 0's second block -> 3, about 173 rows in the others -> 4 and 2)
     for key in ("routes", "slots", "contributions", "output"):
         np.testing.assert_array_equal(res["bigwaves"][key], res["base"][key], err_msg=key)
 
