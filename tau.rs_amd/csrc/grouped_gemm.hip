@@ -407,6 +407,13 @@ constexpr bool kBigWaveSkip = false;
 #else
 constexpr bool kBigWaveSkip = true;
 #endif
+// -DTAU_FRAG_SKIP: the shipped 256-row tile (64x64 wave tiles) skips padding
+// per 32-row fragment instead of per wave (off by default).
+#ifdef TAU_FRAG_SKIP
+constexpr bool kFragSkip = true;
+#else
+constexpr bool kFragSkip = false;
+#endif
 
 // Pipelined weight-streaming kernel for 16-byte-aligned operands.  Each wave
 // owns NB 16-column blocks (gate and up blocks for SiLU) of one 16-row block;
@@ -890,14 +897,15 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             }
         }
     };
-    if constexpr (kBigWave && kBigWaveSkip && (AM == kAGather || EPI == kEpiScatterWeighted)) {
-        // 128-row wave tiles: padding is a suffix of the block, so the 32-row
-        // fragments holding live rows are a prefix of the wave's MI.  The K
-        // loop runs with the MFMAs and A fragment reads of that prefix only;
-        // the other fragments keep zero accumulators (their rows are written
-        // as zeros or dropped).  The count is wave-uniform and chosen once,
-        // outside the K loop, so the accumulators never move.
-        static_assert(MI == 4, "128-row wave tiles hold four 32-row fragments");
+    if constexpr (((kBigWave && kBigWaveSkip) || (kFragSkip && BM == 256)) &&
+                  (AM == kAGather || EPI == kEpiScatterWeighted)) {
+        // Padding is a suffix of the block, so the 32-row fragments holding
+        // live rows are a prefix of the wave's MI.  The K loop runs with the
+        // MFMAs and A fragment reads of that prefix only; the other fragments
+        // keep zero accumulators (their rows are written as zeros or dropped).
+        // The count is wave-uniform and chosen once, outside the K loop, so
+        // the accumulators never move.
+        static_assert(MI <= 4, "at most four 32-row fragments per wave");
         int nl = 0;
 #pragma unroll
         for (int i = 0; i < MI; ++i) nl += row_src[wm * TM + i * 32] >= 0;
@@ -935,9 +943,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_gemm(GemmArgs p) {
             }
         };
         switch (nl) {
-            case 4: k_loop(std::integral_constant<int, 4>{}); break;
-            case 3: k_loop(std::integral_constant<int, 3>{}); break;
-            case 2: k_loop(std::integral_constant<int, 2>{}); break;
+            case 4: k_loop(std::integral_constant<int, MI < 4 ? MI : 4>{}); break;
+            case 3: k_loop(std::integral_constant<int, MI < 3 ? MI : 3>{}); break;
+            case 2: k_loop(std::integral_constant<int, MI < 2 ? MI : 2>{}); break;
             case 1: k_loop(std::integral_constant<int, 1>{}); break;
             default: k_loop(std::integral_constant<int, 0>{}); break;
         }

@@ -37,7 +37,8 @@ def kernel_resources(tmp_path, defines):
     return out
 
 
-BUILDS = {"default": [], "big_waves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"]}
+BUILDS = {"default": [], "big_waves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"],
+          "frag_skip": ["-DTAU_FRAG_SKIP"]}
 
 
 @pytest.fixture(scope="module")

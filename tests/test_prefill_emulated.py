@@ -15,7 +15,8 @@ routing gives both full and nearly empty 256-row blocks.  Checks:
     scalar base, the variant whose one GPU run faulted),
     -DTAU_SPLIT_ROWS=32 / 64 / 128 (lightly filled blocks on the
     weight-streaming kernel or the shorter MFMA tile in a second launch) and
-    the 128x128 tiles with the 64-row split reproduce the shipped build's activated rows, contributions
+    the 128x128 tiles with the 64-row split, and -DTAU_FRAG_SKIP (the shipped
+    tile skipping padding per 32-row fragment) reproduce the shipped build's activated rows, contributions
     and output bit for bit: per output element they issue the same MFMA
     sequence, so any difference is an addressing or scheduling bug (the
     32-row split computes its blocks with 16x16x32 MFMAs, whose internal
@@ -38,7 +39,7 @@ SOURCES = ["combine.cpp", "decode.cpp", "decode_layer.cpp", "decode_moe.cpp", "e
            "grouped_gemm.cpp", "moe.cpp", "norm.cpp", "router.cpp", "routing.cpp"]
 VARIANTS = {"base": [], "bigwaves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"],
             "split128": ["-DTAU_SPLIT_ROWS=128"], "split32": ["-DTAU_SPLIT_ROWS=32"],
-            "bigwaves_split64": ["-DTAU_M256_BIG_WAVES", "-DTAU_SPLIT_ROWS=64"]}
+            "bigwaves_split64": ["-DTAU_M256_BIG_WAVES", "-DTAU_SPLIT_ROWS=64"], "fragskip": ["-DTAU_FRAG_SKIP"]}
 
 
 @pytest.fixture(scope="module")
@@ -131,7 +132,7 @@ def test_256_row_tiles_and_variants(bins, oracle, layout):
     meta = check_against_oracle(oracle, base, x, logits, gu, dn, K, 256)
     counts = meta[:E]
     assert counts.max() > 128 and (counts[counts > 0] <= 64).any()  # both kinds of block
-    for v in ("bigwaves", "split32", "split64", "split128", "bigwaves_split64"):
+    for v in ("bigwaves", "split32", "split64", "split128", "bigwaves_split64", "fragskip"):
         res = run(bins, v, x, logits, gu, dn, K, 256, layout)
         for key in ("routes", "meta", "slots", "tiles", "contributions", "output"):
             np.testing.assert_array_equal(res[key].view(np.uint32) if res[key].dtype == np.float32 else res[key],
@@ -164,15 +165,16 @@ def test_benchmark_layer_dims(bins, oracle, H, I, T):
     import concurrent.futures
     E, K = 3, 2
     x, logits, gu, dn = layer(5, T, H, I, E)
-    with concurrent.futures.ThreadPoolExecutor(2) as ex:
-        futs = {v: ex.submit(run, bins, v, x, logits, gu, dn, K, 256, 1) for v in ("base", "bigwaves")}
+    with concurrent.futures.ThreadPoolExecutor(3) as ex:
+        futs = {v: ex.submit(run, bins, v, x, logits, gu, dn, K, 256, 1) for v in ("base", "bigwaves", "fragskip")}
         res = {v: f.result() for v, f in futs.items()}
     meta = check_against_oracle(oracle, res["base"], x, logits, gu, dn, K, 256)
     assert meta[0] > 256 and meta[0] % 256 <= 96  # a full block and a partly empty one
     # 128-row wave tiles see 0 to 4 live 32-row fragments across the blocks
     # (c3 sizes: about 90 rows in expert 0's second block -> 3, about 173 rows in the others -> 4 and 2)
-    for key in ("routes", "slots", "contributions", "output"):
-        np.testing.assert_array_equal(res["bigwaves"][key], res["base"][key], err_msg=key)
+    for v in ("bigwaves", "fragskip"):
+        for key in ("routes", "slots", "contributions", "output"):
+            np.testing.assert_array_equal(res[v][key], res["base"][key], err_msg=f"{v}: {key}")
 
 
 def test_folded_shared_expert_c4_dims(bins, oracle):
