@@ -39,7 +39,8 @@ SOURCES = ["combine.cpp", "decode.cpp", "decode_layer.cpp", "decode_moe.cpp", "e
            "grouped_gemm.cpp", "moe.cpp", "norm.cpp", "router.cpp", "routing.cpp"]
 VARIANTS = {"base": [], "bigwaves": ["-DTAU_M256_BIG_WAVES"], "split64": ["-DTAU_SPLIT_ROWS=64"],
             "split128": ["-DTAU_SPLIT_ROWS=128"], "split32": ["-DTAU_SPLIT_ROWS=32"],
-            "bigwaves_split64": ["-DTAU_M256_BIG_WAVES", "-DTAU_SPLIT_ROWS=64"], "fragskip": ["-DTAU_FRAG_SKIP"]}
+            "bigwaves_split64": ["-DTAU_M256_BIG_WAVES", "-DTAU_SPLIT_ROWS=64"], "fragskip": ["-DTAU_FRAG_SKIP"],
+            "bigwaves_noskip": ["-DTAU_M256_BIG_WAVES", "-DTAU_BIG_WAVE_NO_SKIP"]}
 
 
 @pytest.fixture(scope="module")
@@ -92,7 +93,8 @@ def run(bins, which, x, logits, gu, dn, K, M, layout, bf16_logits=True, shared=0
     return {"routes": take(np.float32, T * 2 * K).reshape(T, 2 * K), "meta": take(np.int32, 2 * E + 2),
             "offsets": take(np.int32, E + 1), "slots": take(np.int32, cap), "tiles": take(np.int32, cap // M),
             "activated": take(np.uint16, cap * I).reshape(cap, I), "contributions": take(np.uint16, T * K * H),
-            "output": take(np.uint16, T * H).reshape(T, H), "cap": int(cap)}
+            "output": take(np.uint16, T * H).reshape(T, H), "cap": int(cap),
+            "counts": dict(zip(("mfma16", "mfma32", "dma16"), take(np.int64, 3).tolist()))}
 
 
 def layer(seed, T, H, I, E, skew=True):
@@ -262,3 +264,44 @@ def test_full_size_routing_and_dispatch(bins, oracle, tau, T, E, K, shared, bias
         split = run(bins, "split32", x, logits, gu, dn, K, M, 0, shared=shared)
         for key in ("routes", "slots", "contributions", "output"):
             np.testing.assert_array_equal(split[key], res[key], err_msg=key)
+
+
+def test_issued_mfma_work_matches_the_plan(bins, oracle):
+    """The MFMA work the 256-row tiles issue, counted in the emulator, equals
+    what the dispatch plan implies, on c3's token, expert and top-k counts with
+    its N(0,1) router bias (hidden = intermediate = 64 keep it cheap; one
+    64-deep K step and one column tile per projection):
+      * shipped 4x4 waves (64x64 wave tiles): a wave runs its 16 MFMAs per K
+        step unless its 64 rows are all padding -> 64 * ceil(live/64) per block;
+      * -DTAU_FRAG_SKIP and the 128x128 wave tiles: MFMAs only for 32-row
+        fragments holding a live row -> 32 * ceil(live/32) per block;
+      * the 128x128 wave tiles without the skip: 256 per block.
+    At these sizes useful work is one MFMA per assignment per projection, so
+    the ratios are the padding overheads quoted for c3 (about 1.14x, 1.07x and
+    1.63x)."""
+    T, E, K, H, I = 4096, 128, 8, 64, 64
+    rng = np.random.default_rng(2)
+    x = from_bits(bf16_bits(rng.standard_normal((T, H))))
+    gu = from_bits(bf16_bits(rng.standard_normal((E, 2 * I, H)) * 0.05))
+    dn = from_bits(bf16_bits(rng.standard_normal((E, H, I)) * 0.05))
+    logits = rng.standard_normal((T, E)).astype(np.float32) + rng.standard_normal(E).astype(np.float32)
+    logits = from_bits(bf16_bits(logits))
+    import concurrent.futures
+    builds = ("base", "fragskip", "bigwaves", "bigwaves_noskip")
+    with concurrent.futures.ThreadPoolExecutor(4) as ex:
+        futs = {v: ex.submit(run, bins, v, x, logits, gu, dn, K, 256, 0) for v in builds}
+        res = {v: f.result() for v, f in futs.items()}
+    counts = res["base"]["meta"][:E]
+    lives = [min(256, n - b) for n in counts for b in range(0, n, 256)]
+    per_block = {"base": lambda l: 64 * -(-l // 64), "fragskip": lambda l: 32 * -(-l // 32),
+                 "bigwaves": lambda l: 32 * -(-l // 32), "bigwaves_noskip": lambda l: 256}
+    projections = 2  # gate_up and down: one K step and one column tile each at these sizes
+    for v in builds:
+        expected = projections * sum(per_block[v](l) for l in lives)
+        assert res[v]["counts"]["mfma32"] == expected, (v, res[v]["counts"], expected)
+        assert res[v]["counts"]["mfma16"] == 0
+        np.testing.assert_array_equal(res[v]["output"], res["base"]["output"], err_msg=v)
+    useful = projections * T * K
+    ratio = {v: res[v]["counts"]["mfma32"] / useful for v in builds}
+    assert ratio["fragskip"] == ratio["bigwaves"] < ratio["base"] < ratio["bigwaves_noskip"]
+    print("issued / useful MFMA rows:", {v: round(r, 3) for v, r in ratio.items()})

@@ -272,6 +272,12 @@ inline int emu_readlane(int v, int l) { return (int)emu::exchange((uint32_t)v, l
 #define __builtin_amdgcn_readlane(v, l) emu_readlane(v, l)
 #define __builtin_amdgcn_readfirstlane(v) emu_readlane(v, 0)
 
+namespace emu {
+// Wave-instruction counts since the process started (counted by lane 0):
+// MFMAs of each shape and direct-to-LDS copies.
+inline long long count_mfma16 = 0, count_mfma32 = 0, count_dma16 = 0;
+}  // namespace emu
+
 // v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][8(l/16)..+8], B[8(l/16)..+8][l%16]
 // and D[4(l/16)+q][l%16], q = 0..3.
 typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
@@ -279,6 +285,7 @@ typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
 inline emu_f32x4 emu_mfma_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c) {
     emu::Wave& w = emu::wave();
     const int l = emu::lane();
+    if (l == 0) ++emu::count_mfma16;
     std::memcpy(w.a[l], &a, 16);
     std::memcpy(w.b[l], &b, 16);
     emu::arrive(w.bar);
@@ -307,6 +314,7 @@ typedef float emu_f32x16 __attribute__((ext_vector_type(16)));
 inline emu_f32x16 emu_mfma_32x32x16_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x16 c) {
     emu::Wave& w = emu::wave();
     const int l = emu::lane();
+    if (l == 0) ++emu::count_mfma32;
     std::memcpy(w.a[l], &a, 16);
     std::memcpy(w.b[l], &b, 16);
     emu::arrive(w.bar);
@@ -336,6 +344,7 @@ namespace emu {
 // wave's LDS base (the first lane's destination) + 16 * lane.
 inline void dma16(const uint16_t* src, uint16_t* lds) {
     uint16_t* base = __shfl(lds, 0);
+    if (lane() == 0) ++count_dma16;
     std::memcpy(base + 8 * lane(), src, 16);
 }
 }  // namespace emu

@@ -11,7 +11,8 @@
 //            from those routes with E+1 experts and K+1 picks)
 //   out.bin: int32 status, capacity; routes [T,2K] f32; meta [2E+2], offsets [E+1],
 //            slots [cap], tiles [cap/tile_rows] int32; activated [cap,I],
-//            contributions [T*K,H], output [T,H] u16
+//            contributions [T*K,H], output [T,H] u16; int64 counts of the emulated
+//            wave instructions: 16x16x32 MFMAs, 32x32x16 MFMAs, direct-to-LDS copies
 // Every device buffer lives in one arena mapped at 0x7e0080000000, so the low
 // 32 bits of every address have bit 31 set: a 64-bit address rebuilt from two
 // 32-bit words with the low word sign-extended (the fault of the 128x128
@@ -23,6 +24,7 @@
 #include <vector>
 
 #include "../../include/tau_moe.h"
+#include "hip/hip_runtime.h"  // the emulator's instruction counts
 
 static char* g_arena = nullptr;
 static size_t g_used = 0;
@@ -97,6 +99,8 @@ int main(int argc, char** argv) {
     write(o, act);
     write(o, con);
     write(o, out);
+    const long long counts[3] = {emu::count_mfma16, emu::count_mfma32, emu::count_dma16};
+    std::fwrite(counts, sizeof counts[0], 3, o);
     std::fclose(o);
     return 0;
 }
