@@ -278,7 +278,8 @@ def test_issued_mfma_work_matches_the_plan(bins, oracle):
       * the 128x128 wave tiles without the skip: 256 per block.
     At these sizes useful work is one MFMA per assignment per projection, so
     the ratios are the padding overheads quoted for c3 (about 1.14x, 1.07x and
-    1.63x)."""
+    1.63x).  The operand copies are counted too: every build stages the whole
+    weight panel and skips A's all-padding 8-row groups."""
     T, E, K, H, I = 4096, 128, 8, 64, 64
     rng = np.random.default_rng(2)
     x = from_bits(bf16_bits(rng.standard_normal((T, H))))
@@ -300,6 +301,10 @@ def test_issued_mfma_work_matches_the_plan(bins, oracle):
         expected = projections * sum(per_block[v](l) for l in lives)
         assert res[v]["counts"]["mfma32"] == expected, (v, res[v]["counts"], expected)
         assert res[v]["counts"]["mfma16"] == 0
+        # direct-to-LDS copies (1 KB per wave instruction): per block and K step
+        # the 256x64 weight panel (32) and the A rows in 8-row groups, all-padding
+        # groups skipped (ceil(live/8))
+        assert res[v]["counts"]["dma16"] == projections * sum(32 + -(-l // 8) for l in lives), v
         np.testing.assert_array_equal(res[v]["output"], res["base"]["output"], err_msg=v)
     useful = projections * T * K
     ratio = {v: res[v]["counts"]["mfma32"] / useful for v in builds}
